@@ -1,0 +1,110 @@
+/*
+ * trellis_amd.h — C ABI of the MI355X (gfx950) trellis packed-linear library.
+ *
+ * Plain C: device pointers, sizes and an opaque stream handle (a hipStream_t passed
+ * as void*; NULL is the default stream). No torch or HIP types appear here.
+ *
+ * Semantics follow the reference's packed linear: y = restore(decode(bits)) @ x, with
+ * the incoherence-processing transforms folded onto the activations
+ * (web/packed.js:163-182):
+ *     xf = Hb_k(isc_scaled * su * x);  t = Zq @ xf;  y = sv * osc * Hb_n(t)
+ * where Zq is decoded from the packed K-bit trellis stream (src/trellis/qtip.py:82-110,
+ * web/kernels.js:115-122), Hb_d is the normalized block-diagonal Sylvester Hadamard
+ * with block fit(d,128) (qtip.py:200-223) and isc_scaled = f32(isc) * scale, folded at
+ * load as web/packed.js:51-52 does.
+ *
+ * Conventions
+ *  - The caller owns every buffer. No call allocates device memory.
+ *  - Calls are ordered on `stream` and never synchronize the host.
+ *  - Calls that share one workspace must not overlap (use one workspace per stream).
+ *  - Errors are returned as trellis_status codes; trellis_strerror() names them.
+ */
+#ifndef TRELLIS_AMD_H
+#define TRELLIS_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Codebook ids (qtip.py:32-56). The reference manifest has no codebook field and
+ * hard-codes MCG (export_packed.py:42); absent means TRELLIS_CB_MCG. */
+enum trellis_codebook {
+  TRELLIS_CB_MCG = 0,   /* x*0xCBAC1FED, lop3, fp16 halves summed in fp32 (qtip.py:48-53) */
+  TRELLIS_CB_3INST = 1, /* x*89226354+64248484, lop3, fp16 halves (qtip.py:40-45) */
+  TRELLIS_CB_1MAD = 2   /* x*34038481+76625530, byte sum, (y-510)/147.800537109375 (qtip.py:32-37) */
+};
+
+enum trellis_dtype { TRELLIS_F32 = 0, TRELLIS_F16 = 1 };
+
+typedef enum trellis_status {
+  TRELLIS_OK = 0,
+  TRELLIS_ERR_NULL = 1,        /* a required pointer is NULL */
+  TRELLIS_ERR_SHAPE = 2,       /* n or k not a positive multiple of 16 */
+  TRELLIS_ERR_BLOCK = 3,       /* Hadamard block not a power of 2 in [16,128] dividing the dim */
+  TRELLIS_ERR_K = 4,           /* bits/weight outside {2,3,4} */
+  TRELLIS_ERR_V = 5,           /* vector dimension other than 1 */
+  TRELLIS_ERR_CODEBOOK = 6,    /* unknown codebook id */
+  TRELLIS_ERR_NWORDS = 7,      /* nwords != 256*K/32 */
+  TRELLIS_ERR_ALIGN = 8,       /* bits not 16-byte aligned, or a stride too small */
+  TRELLIS_ERR_DTYPE = 9,       /* unsupported x/y dtype */
+  TRELLIS_ERR_WORKSPACE = 10,  /* workspace missing or smaller than trellis_workspace_bytes */
+  TRELLIS_ERR_BATCH = 11,      /* batch < 1 */
+  TRELLIS_ERR_RANGE = 12,      /* tile range outside the matrix */
+  TRELLIS_ERR_LAUNCH = 13      /* the HIP runtime rejected a launch */
+} trellis_status;
+
+/* One packed trellis linear as the loader record holds it (web/packed.js:53-62,
+ * 93-103): device pointers to the packed words and f32 metadata. */
+typedef struct trellis_desc {
+  const uint32_t *bits;      /* u32 [ntiles * nwords], tile = (row/16)*tiles_in + col/16 */
+  const float *su;           /* [k_in]  input-dim signs */
+  const float *sv;           /* [n_out] output-dim signs */
+  const float *isc_scaled;   /* [k_in]  f32(isc) * scale */
+  const float *osc;          /* [n_out] per-out-channel scale */
+  int32_t n_out;             /* rows, multiple of 16 */
+  int32_t k_in;              /* cols, multiple of 16 */
+  int32_t K;                 /* bits per weight: 2, 3 or 4 */
+  int32_t V;                 /* weights per trellis step: 1 */
+  int32_t codebook;          /* enum trellis_codebook */
+  int32_t block_in;          /* fit(k_in, 128) */
+  int32_t block_out;         /* fit(n_out, 128) (web/packed.js:173-176) */
+  int32_t nwords;            /* 256*K/32 words per tile */
+} trellis_desc;
+
+/* Number of workspace bytes trellis_packed_linear needs for this layer and batch.
+ * The workspace must be zero-filled once when allocated; every call leaves its
+ * counters at zero again. Replaces the per-call scratch f32buf allocations of
+ * web/packed.js:165-180. */
+int trellis_workspace_bytes(const trellis_desc *W, int batch, size_t *bytes);
+
+/* y[b, :] = W_hat @ x[b, :] for b < batch. Replaces PackedOps.linear
+ * (web/packed.js:163-182) and its Python mirror linear() (scripts/run_packed_headless.py:87-99).
+ *   x: [batch, k_in] with row stride ldx elements, dtype x_dtype (f16 or f32)
+ *   y: [batch, n_out] with row stride ldy elements, dtype y_dtype (f16 or f32)
+ * Batch < 16 runs the decode-GEMV kernel; batch >= 16 the decode-to-LDS MFMA kernel. */
+int trellis_packed_linear(const trellis_desc *W, const void *x, int64_t ldx, int batch,
+                          int x_dtype, void *y, int64_t ldy, int y_dtype, void *workspace,
+                          size_t ws_bytes, void *stream);
+
+/* Decode z-space tiles [tile_begin, tile_begin+ntiles) to fp32, 256 values per tile in
+ * tile order t = (row%16)*16 + col%16. The bit-exact probe of the decode: restates
+ * decode_window over the packed stream (qtip.py:82-110, web/kernels.js:115-122) with the
+ * codebooks of qtip.py:32-53, using the same window/codebook code as the matmul
+ * kernels. */
+int trellis_decode_tiles(const trellis_desc *W, uint32_t tile_begin, uint32_t ntiles,
+                         float *out, void *stream);
+
+/* Human-readable name of a status code. */
+const char *trellis_strerror(int status);
+
+/* Library version string (no reference counterpart). */
+const char *trellis_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TRELLIS_AMD_H */

@@ -1,0 +1,64 @@
+"""Packed format writer/reader (trellis-everywhere_amd/format.py; reference
+scripts/export_packed.py:45-63, export_packed_8b.py:65-81, web/packed.js:14-114)."""
+import json
+import os
+
+import numpy as np
+
+from oracle import trellis_np as tn
+
+
+def _rec(te, n, k, K, seed, cb="mcg"):
+    bits, r = tn.synthetic_record(n, k, K, seed, codebook=cb)
+    return te.PackedRecord(n, k, K, bits, r.su, r.sv, r.isc, r.osc, float(r.scale), codebook=cb)
+
+
+def test_roundtrip_single_blob(te, tmp_path):
+    recs = {"model.layers.0.mlp.up_proj": _rec(te, 64, 32, 3, 1),
+            "model.layers.0.mlp.down_proj": _rec(te, 32, 64, 3, 2, cb="3inst")}
+    dense = {"model.norm.weight": np.ones(32, np.float16)}
+    te.write_packed(str(tmp_path), recs, dense, config={"K": 3})
+    man = json.load(open(tmp_path / "manifest.json"))
+    m = man["model.layers.0.mlp.up_proj"]
+    # manifest keys of export_packed.py:62-63
+    assert m == {"quant": True, "n_out": 64, "k_in": 32, "K": 3, "block": 32,
+                 "tiles_out": 4, "tiles_in": 2}
+    assert man["model.layers.0.mlp.up_proj.bits"]["dtype"] == "u32"
+    assert man["model.layers.0.mlp.up_proj.bits"]["shape"] == [8, 24]
+    assert man["model.layers.0.mlp.up_proj.scale"]["dtype"] == "f32"
+    assert man["model.layers.0.mlp.down_proj"]["codebook"] == "3inst"
+    got, gdense, cfg = te.read_packed(str(tmp_path))
+    assert cfg == {"K": 3}
+    for name, r in recs.items():
+        g = got[name]
+        assert np.array_equal(g.bits, r.bits) and g.codebook == r.codebook
+        for f in ("su", "sv", "isc", "osc"):
+            assert np.array_equal(getattr(g, f), getattr(r, f))
+        assert np.float32(g.scale) == np.float32(r.scale)
+    assert np.array_equal(gdense["model.norm.weight"], dense["model.norm.weight"])
+
+
+def test_blob_bytes_match_reference_layout(te, tmp_path):
+    """Offsets are consecutive in put() order: bits, su, sv, isc, osc, scale."""
+    r = _rec(te, 32, 32, 3, 3)
+    te.write_packed(str(tmp_path), {"l": r})
+    man = json.load(open(tmp_path / "manifest.json"))
+    blob = open(tmp_path / "weights.bin", "rb").read()
+    off = 0
+    for key, nbytes in (("bits", r.bits.nbytes), ("su", 64), ("sv", 64), ("isc", 64),
+                        ("osc", 64), ("scale", 4)):
+        assert man[f"l.{key}"]["offset"] == off
+        off += nbytes
+    assert len(blob) == off
+    assert blob[:r.bits.nbytes] == r.bits.astype("<u4").tobytes()
+
+
+def test_sharded_manifest(te, tmp_path):
+    r = _rec(te, 32, 48, 2, 4)
+    te.write_packed(str(tmp_path), {"model.layers.3.self_attn.q_proj.weight": r},
+                    shard="layer_03.bin")
+    man = json.load(open(tmp_path / "manifest.json"))
+    assert all(m["shard"] == "layer_03.bin" for m in man.values())
+    assert not os.path.exists(tmp_path / "weights.bin")
+    got, _, _ = te.read_packed(str(tmp_path))
+    assert np.array_equal(got["model.layers.3.self_attn.q_proj.weight"].bits, r.bits)

@@ -1,0 +1,175 @@
+"""GPU parity of the HIP kernels against the CPU oracle, through the C ABI.
+
+Bars: decoded tiles bit-exact; matmul max|got-ref|/(max|ref|+1e-6) <= 1e-3 against the
+float64 oracle W_hat @ x (validate_packed_linear.py:66-69 metric and threshold).
+"""
+import functools
+import os
+import sys
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import trellis_np as tn
+
+pytestmark = pytest.mark.gpu
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+TOL = 1e-3
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def make_linear(te, bits, rec, device):
+    r = te.PackedRecord(rec.n, rec.k, rec.K, bits, rec.su, rec.sv, rec.isc, rec.osc,
+                        float(rec.scale), codebook=rec.codebook)
+    return te.PackedLinear(r, device=device)
+
+
+def fixture(name):
+    d = np.load(os.path.join(GOLD, name + ".npz"))
+    n, k = d["sv"].shape[0], d["su"].shape[0]
+    rec = tn.IPRecord(n, k, int(d["K"]), d["su"], d["sv"], d["isc"], d["osc"], d["scale"],
+                      codebook=str(d["codebook"]))
+    return d, rec
+
+
+# ------------------------------------------------------------------ decode bit-exactness
+@pytest.mark.parametrize("K", [2, 3, 4])
+@pytest.mark.parametrize("cb", ["mcg", "3inst", "1mad"])
+def test_decode_tiles_golden_bit_exact(te, gpu_device, K, cb):
+    _say(f"[decode golden] K={K} cb={cb}")
+    d, rec = fixture(f"synth_K{K}_{cb}")
+    lin = make_linear(te, d["bits"], rec, gpu_device)
+    got = lin.decode_tiles().cpu().numpy()
+    want = tn.decode_packed_tiles(d["bits"], K, cb)
+    assert got.view(np.uint32).tobytes() == want.view(np.uint32).tobytes()
+    assert np.array_equal(got[:8], d["tiles_head"])
+
+
+@pytest.mark.parametrize("K", [2, 3, 4])
+@pytest.mark.parametrize("cb", ["mcg", "3inst", "1mad"])
+def test_decode_tiles_all_states_bit_exact(te, gpu_device, K, cb):
+    """A 4096x1024 random record (16384 tiles, 4.2M windows) covers every 16-bit state
+    many times over; compare every decoded value bitwise, and a sub-range call."""
+    _say(f"[decode large] K={K} cb={cb}")
+    bits, rec = tn.synthetic_record(1024, 4096, K, seed=K * 7 + tn.CODEBOOK_IDS[cb], codebook=cb)
+    lin = make_linear(te, bits, rec, gpu_device)
+    got = lin.decode_tiles().cpu().numpy()
+    want = tn.decode_packed_tiles(bits, K, cb)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    sub = lin.decode_tiles(1000, 77).cpu().numpy()
+    assert np.array_equal(sub.view(np.uint32), want[1000:1077].view(np.uint32))
+
+
+# ------------------------------------------------------------------ packed linear
+def test_config1_golden(te, gpu_device):
+    """SmolLM2 up_proj 576->1536, K=3, 3INST, real Viterbi encode."""
+    _say("[linear] config1 golden")
+    d, rec = fixture("config1_smollm2_up")
+    lin = make_linear(te, d["bits"], rec, gpu_device)
+    x = torch.from_numpy(d["x"]).to(gpu_device)
+    for b in (1, 2):
+        y = lin(x[:b]).cpu().numpy()
+        assert tn.rel_err(y, d["y_ref"][:b]) < TOL
+    y1 = lin(x[0]).cpu().numpy()
+    assert y1.shape == (1536,)
+    assert tn.rel_err(y1, d["y_ref"][0]) < TOL
+
+
+@pytest.mark.parametrize("K", [2, 3, 4])
+@pytest.mark.parametrize("cb", ["mcg", "3inst", "1mad"])
+def test_linear_golden_synth(te, gpu_device, K, cb):
+    _say(f"[linear golden] K={K} cb={cb}")
+    d, rec = fixture(f"synth_K{K}_{cb}")
+    lin = make_linear(te, d["bits"], rec, gpu_device)
+    y = lin(torch.from_numpy(d["x"]).to(gpu_device)).cpu().numpy()
+    assert tn.rel_err(y, d["y_ref"]) < TOL
+
+
+@functools.lru_cache(maxsize=4)
+def _record_and_w_hat(n, k, K, cb):
+    bits, rec = tn.synthetic_record(n, k, K, seed=n * 3 + k + K, codebook=cb)
+    return bits, rec, tn.w_hat_from_record(bits, rec)
+
+
+@pytest.mark.parametrize("n,k,K,cb", [
+    (256, 512, 3, "mcg"), (1536, 576, 3, "3inst"), (576, 1536, 3, "mcg"), (2048, 6144, 3, "mcg"),
+    (6144, 2048, 3, "mcg"), (128, 4096, 2, "mcg"), (384, 1024, 4, "3inst"), (208, 336, 3, "1mad"),
+])
+@pytest.mark.parametrize("batch", [1, 3, 8])
+def test_linear_vs_oracle(te, gpu_device, n, k, K, cb, batch):
+    _say(f"[linear] n={n} k={k} K={K} cb={cb} batch={batch}")
+    bits, rec, W = _record_and_w_hat(n, k, K, cb)
+    lin = make_linear(te, bits, rec, gpu_device)
+    x = np.random.default_rng(batch).standard_normal((batch, k)).astype(np.float16)
+    want = x.astype(np.float64) @ W.T
+    y = lin(torch.from_numpy(x).to(gpu_device)).cpu().numpy()
+    assert tn.rel_err(y, want) < TOL
+
+
+@pytest.mark.parametrize("xdt,ydt", [(torch.float32, torch.float32), (torch.float16, torch.float16),
+                                     (torch.float32, torch.float16)])
+def test_dtypes_and_strides(te, gpu_device, xdt, ydt):
+    _say(f"[linear dtypes] x={xdt} y={ydt}")
+    n, k = 512, 1024
+    bits, rec = tn.synthetic_record(n, k, 3, seed=11)
+    lin = make_linear(te, bits, rec, gpu_device)
+    xs = np.random.default_rng(0).standard_normal((4, k + 64)).astype(np.float32)
+    xt = torch.from_numpy(xs).to(gpu_device).to(xdt)[:, :k]      # row stride k+64
+    out = torch.zeros((4, n + 32), dtype=ydt, device=gpu_device)[:, :n]
+    lin.forward(xt, out=out)
+    want = tn.packed_linear_ref(bits, rec, xt.float().cpu().numpy())
+    assert tn.rel_err(out.float().cpu().numpy(), want) < (2e-3 if ydt == torch.float16 else TOL)
+
+
+def test_repeat_calls_deterministic_and_ticket_reset(te, gpu_device):
+    """Split-K tickets reset themselves: repeated calls give bit-identical results."""
+    _say("[linear] determinism")
+    bits, rec = tn.synthetic_record(1024, 4096, 3, seed=5)
+    lin = make_linear(te, bits, rec, gpu_device)
+    x = torch.randn(4096, device=gpu_device, dtype=torch.float16)
+    ys = [lin(x).clone() for _ in range(5)]
+    torch.cuda.synchronize()
+    for y in ys[1:]:
+        assert torch.equal(y, ys[0])
+    want = tn.packed_linear_ref(bits, rec, x.cpu().numpy())
+    assert tn.rel_err(ys[0].cpu().numpy(), want) < TOL
+
+
+def _oracle_block_rows(bits, rec, ob, x):
+    """Oracle for output rows [128*ob, 128*ob+128): those rows depend only on their own
+    8 bands (the out-dim Hadamard block is 128)."""
+    tin = rec.k // 16
+    sub_bits = bits[ob * 8 * tin:(ob + 1) * 8 * tin]
+    sl = slice(ob * 128, ob * 128 + 128)
+    sub = tn.IPRecord(128, rec.k, rec.K, rec.su, rec.sv[sl], rec.isc, rec.osc[sl], rec.scale,
+                      codebook=rec.codebook)
+    return tn.packed_linear_ref(sub_bits, sub, x)
+
+
+@pytest.mark.parametrize("name,n,k", [("q_proj", 4096, 4096), ("k_proj", 1024, 4096),
+                                      ("gate_proj", 12288, 4096), ("down_proj", 4096, 12288)])
+def test_qwen3_8b_shapes_sampled_blocks(te, gpu_device, name, n, k):
+    """BASELINE configs[2] at full size: every output row checked would need a 50M
+    weight dense oracle, so three 128-row blocks (first, middle, last) are checked
+    exactly and the rest by linearity: f(a*x1 + b*x2) = a f(x1) + b f(x2)."""
+    _say(f"[8B] {name} {n}x{k}")
+    bits, rec = tn.synthetic_record(n, k, 3, seed=zlib.crc32(name.encode()))
+    lin = make_linear(te, bits, rec, gpu_device)
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((1, k)).astype(np.float16)
+    y = lin(torch.from_numpy(x).to(gpu_device)).cpu().numpy()[0]
+    for ob in (0, (n // 128) // 2, n // 128 - 1):
+        want = _oracle_block_rows(bits, rec, ob, x)[0]
+        assert tn.rel_err(y[ob * 128:(ob + 1) * 128], want) < TOL
+    x1 = torch.randn(k, device=gpu_device)
+    x2 = torch.randn(k, device=gpu_device)
+    lhs = lin(0.75 * x1 - 1.5 * x2)
+    rhs = 0.75 * lin(x1) - 1.5 * lin(x2)
+    assert (lhs - rhs).abs().max().item() / rhs.abs().max().item() < TOL

@@ -1,0 +1,155 @@
+"""Host side of the packed trellis linear: device upload (the loader record of
+web/packed.js:46-62, 88-103) and the packed-linear call (PackedOps.linear,
+web/packed.js:163-182), dispatched to the gfx950 kernels through the C ABI.
+
+PyTorch provides device memory and the current stream only; all compute runs in
+libtrellis_amd.so. There is no CPU fallback: without the library every call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+
+from . import _capi
+from .format import PackedRecord, fit_block
+
+
+def _ptr(t: torch.Tensor) -> int:
+    return t.data_ptr()
+
+
+class PackedLinear:
+    """One packed trellis linear resident on a GPU.
+
+    Load-time fold (web/packed.js:51-52, 91-92): su, sv, osc are upcast f16 -> f32 and
+    isc_scaled = f32(isc) * scale in fp32. The kernels then compute
+    y = sv * osc * Hb_n(Zq @ Hb_k(isc_scaled * su * x)) = restore(decode(bits)) @ x.
+    """
+
+    def __init__(self, rec: PackedRecord, device="cuda", name: str = ""):
+        rec.validate()
+        bits = np.ascontiguousarray(rec.bits, np.uint32).view(np.int32)
+        dev = torch.device(device)
+        f32 = lambda a: torch.from_numpy(np.asarray(a, np.float16).astype(np.float32)).to(dev)
+        isc_scaled = (np.asarray(rec.isc, np.float16).astype(np.float32) * np.float32(rec.scale))
+        self._init(rec.n_out, rec.k_in, rec.K, rec.V, rec.codebook, float(np.float32(rec.scale)),
+                   torch.from_numpy(bits.copy()).to(dev), f32(rec.su), f32(rec.sv),
+                   torch.from_numpy(isc_scaled.astype(np.float32)).to(dev), f32(rec.osc), name)
+
+    @classmethod
+    def from_device(cls, n_out, k_in, K, bits, su, sv, isc_scaled, osc, scale=1.0,
+                    codebook="mcg", V=1, name=""):
+        """Wrap tensors already on the GPU: bits int32/uint32 [ntiles, nwords], f32
+        su/sv/osc and the folded isc_scaled = f32(isc) * scale."""
+        self = cls.__new__(cls)
+        self._init(n_out, k_in, K, V, codebook, float(scale), bits, su, sv, isc_scaled, osc, name)
+        return self
+
+    def _init(self, n_out, k_in, K, V, codebook, scale, bits, su, sv, isc_scaled, osc, name):
+        if codebook not in _capi.CB_IDS:
+            raise ValueError(f"unknown codebook {codebook!r}")
+        self.name = name
+        self.n_out, self.k_in, self.K, self.V = int(n_out), int(k_in), int(K), int(V)
+        self.codebook = codebook
+        self.scale = scale
+        self.block_in, self.block_out = fit_block(self.k_in), fit_block(self.n_out)
+        self.nwords = (256 * self.K + 31) // 32
+        self.device = bits.device
+        ntiles = (self.n_out // 16) * (self.k_in // 16)
+        if tuple(bits.shape) != (ntiles, self.nwords) or not bits.is_contiguous():
+            raise ValueError(f"bits must be contiguous [{ntiles}, {self.nwords}]")
+        for nm, t, ln in (("su", su, self.k_in), ("isc_scaled", isc_scaled, self.k_in),
+                          ("sv", sv, self.n_out), ("osc", osc, self.n_out)):
+            if t.dtype != torch.float32 or t.numel() != ln or t.device != self.device:
+                raise ValueError(f"{nm} must be a float32 [{ln}] tensor on {self.device}")
+        self.bits, self.su, self.sv, self.isc_scaled, self.osc = (
+            bits, su.contiguous(), sv.contiguous(), isc_scaled.contiguous(), osc.contiguous())
+        self.desc = _capi.TrellisDesc(
+            _ptr(self.bits), _ptr(self.su), _ptr(self.sv), _ptr(self.isc_scaled), _ptr(self.osc),
+            self.n_out, self.k_in, self.K, self.V, _capi.CB_IDS[self.codebook],
+            self.block_in, self.block_out, self.nwords)
+        self._ws = None
+
+    @property
+    def packed_bytes(self) -> int:
+        return self.bits.numel() * 4
+
+    # ------------------------------------------------------------------ workspace
+    def workspace_bytes(self, batch: int) -> int:
+        lib = _capi.load()
+        n = ctypes.c_size_t(0)
+        _capi.check(lib.trellis_workspace_bytes(ctypes.byref(self.desc), int(batch), ctypes.byref(n)))
+        return int(n.value)
+
+    def _workspace(self, batch: int) -> torch.Tensor:
+        need = self.workspace_bytes(batch)
+        if self._ws is None or self._ws.numel() < need:
+            # zero-filled once; every call leaves the tickets at zero again
+            self._ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=self.device)
+        return self._ws
+
+    # ------------------------------------------------------------------ calls
+    def forward(self, x: torch.Tensor, out: torch.Tensor | None = None,
+                out_dtype: torch.dtype = torch.float32,
+                workspace: torch.Tensor | None = None) -> torch.Tensor:
+        """y = W_hat @ x for x [k_in] or [batch, k_in] (fp16 or fp32, on this device)."""
+        lib = _capi.load()
+        squeeze = x.dim() == 1
+        x2 = x.unsqueeze(0) if squeeze else x
+        if x2.dim() != 2 or x2.shape[1] != self.k_in:
+            raise ValueError(f"x shape {tuple(x.shape)} does not match k_in={self.k_in}")
+        if x2.device != self.device:
+            raise ValueError(f"x on {x2.device}, weights on {self.device}")
+        if x2.dtype not in (torch.float16, torch.float32):
+            raise ValueError(f"x dtype {x2.dtype} not supported")
+        if x2.stride(1) != 1:
+            x2 = x2.contiguous()
+        B = x2.shape[0]
+        if out is None:
+            out = torch.empty((B, self.n_out), dtype=out_dtype, device=self.device)
+        y2 = out.view(B, self.n_out) if out.dim() == 1 else out
+        if y2.dtype not in (torch.float16, torch.float32) or y2.stride(1) != 1:
+            raise ValueError("out must be fp16/fp32 with unit column stride")
+        ws = workspace if workspace is not None else self._workspace(B)
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        st = lib.trellis_packed_linear(
+            ctypes.byref(self.desc), _ptr(x2), x2.stride(0), B,
+            _capi.DT_F16 if x2.dtype == torch.float16 else _capi.DT_F32,
+            _ptr(y2), y2.stride(0), _capi.DT_F16 if y2.dtype == torch.float16 else _capi.DT_F32,
+            _ptr(ws), ws.numel(), ctypes.c_void_p(stream))
+        _capi.check(st)
+        return out[0] if (squeeze and out.dim() == 2) else out
+
+    __call__ = forward
+
+    def decode_tiles(self, tile_begin: int = 0, ntiles: int | None = None) -> torch.Tensor:
+        """fp32 z-space tiles [ntiles, 256] (the bit-exact decode)."""
+        lib = _capi.load()
+        total = (self.n_out // 16) * (self.k_in // 16)
+        nt = total - tile_begin if ntiles is None else ntiles
+        out = torch.empty((nt, 256), dtype=torch.float32, device=self.device)
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        _capi.check(lib.trellis_decode_tiles(ctypes.byref(self.desc), tile_begin, nt, _ptr(out),
+                                             ctypes.c_void_p(stream)))
+        return out
+
+
+class PackedOps:
+    """Mirror of the reference's PackedOps (web/packed.js:130-184): linear(W, x)
+    returns {"y": y, "scale": W.scale}."""
+
+    def linear(self, W: PackedLinear, x: torch.Tensor, out_dtype=torch.float32) -> dict:
+        return {"y": W.forward(x, out_dtype=out_dtype), "scale": W.scale}
+
+
+def load_packed(model_dir: str, device="cuda"):
+    """Mirror of loadPacked / loadPackedSharded (web/packed.js:14-114): returns
+    {"cfg": config, "tensors": {name: PackedLinear | torch.Tensor}}."""
+    from .format import read_packed
+    records, dense, cfg = read_packed(model_dir)
+    tensors = {name: PackedLinear(r, device=device, name=name) for name, r in records.items()}
+    for name, a in dense.items():
+        tensors[name] = torch.from_numpy(np.ascontiguousarray(a)).to(device)
+    return {"cfg": cfg, "tensors": tensors}
