@@ -3,7 +3,8 @@
 Workload: the seven linears of one Qwen3-8B decoder block,
 q 4096->4096, k/v 4096->1024, o 4096->4096, gate/up 4096->12288, down 12288->4096, K=3,
 MCG, packed bits uniform random from a seed, seeded +-1 signs, per-matrix scale, fp16
-N(0,1) activations. One step = the seven packed-linear calls of one block. Weights are
+N(0,1) activations. One step = the seven packed linears of one block in forward order as four launches
+(q/k/v grouped, o, gate/up grouped, down). Weights are
 resident in HBM; to defeat the 256 MB Infinity Cache the steps rotate over `copies`
 distinct blocks (>= 1 GB of packed bits by default).
 
@@ -28,8 +29,12 @@ sys.path.insert(0, ROOT)
 
 LAYERS = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
           ("gate", 12288, 4096), ("up", 12288, 4096), ("down", 4096, 12288)]
+# launches of one block in forward order: linears that share an input run as one group
+# (trellis_packed_linear_group); o waits for attention and down for the MLP activation
+GROUPS = [("qkv", ("q", "k", "v")), ("o", ("o",)), ("gate_up", ("gate", "up")),
+          ("down", ("down",))]
+DOMINANT = "gate_up"   # 2 x 18,874,368 packed bytes per launch
 HBM_PEAK_GBS = 8000.0
-DOMINANT = ("gate", "up", "down")   # 18,874,368 packed bytes per launch each
 
 
 def make_block(te, torch, dev, K, seed, codebook="mcg"):
@@ -122,48 +127,79 @@ def main():
     blocks = [make_block(te, torch, dev, args.K, seed=c) for c in range(copies)]
     B = args.batch
     xs = {name: torch.randn((B, k), device=dev, dtype=torch.float16) for name, _, k in LAYERS}
+    # group members that share an input read the same tensor
+    xs["k"] = xs["v"] = xs["q"]
+    xs["up"] = xs["gate"]
     ys = {name: torch.empty((B, n), device=dev, dtype=torch.float32) for name, n, _ in LAYERS}
-    for blk in blocks:
-        for name, lin in blk.items():
+    groups = [[(gname, te.PackedGroup([blk[m] for m in members]), members)
+               for gname, members in GROUPS] for blk in blocks]
+    for blk, grps in zip(blocks, groups):
+        for lin in blk.values():
             lin._workspace(B)
+        for _, grp, _ in grps:
+            grp._workspace(B)
+
+    def step(s, only=None):
+        for gname, grp, members in groups[s % copies]:
+            if only is None or gname == only:
+                grp.forward([xs[m] for m in members], [ys[m] for m in members])
+
+    def single(s, name):
+        blocks[s % copies][name].forward(xs[name], out=ys[name])
+
+    # warm up eagerly (allocates nothing later), then capture one HIP graph per weight
+    # copy: the four launches of a block replay without per-call host overhead
+    for s in range(max(args.warmup, copies)):
+        step(s)
+        for name, _, _ in LAYERS:
+            single(s, name)
     torch.cuda.synchronize()
 
-    def step(s, events=None):
-        blk = blocks[s % copies]
-        for name, _, _ in LAYERS:
-            if events is not None:
-                e0 = torch.cuda.Event(enable_timing=True)
-                e1 = torch.cuda.Event(enable_timing=True)
-                e0.record()
-                blk[name].forward(xs[name], out=ys[name])
-                e1.record()
-                events.append((name, e0, e1))
-            else:
-                blk[name].forward(xs[name], out=ys[name])
+    def capture(fn):
+        g = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn()
+        torch.cuda.current_stream().wait_stream(side)
+        with torch.cuda.graph(g):
+            fn()
+        return g
 
+    graphs = [capture(lambda c=c: step(c)) for c in range(copies)]
     for s in range(args.warmup):
-        step(s)
+        graphs[s % copies].replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for s in range(args.steps):
-        step(s)
+        graphs[s % copies].replay()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     sec_per_step = (t1 - t0) / args.steps
 
-    # per-launch kernel durations from HIP events on the launch stream (a second timed
-    # pass so the headline pass carries no event overhead)
-    events = []
-    for s in range(args.steps):
-        step(s, events)
-    torch.cuda.synchronize()
-    per = {}
-    for name, e0, e1 in events:
-        per.setdefault(name, []).append(e0.elapsed_time(e1) * 1e3)   # us
-    us_layer = {name: round(statistics.mean(v), 3) for name, v in per.items()}
-    dom = [u for name in DOMINANT for u in per[name]]
-    dom_us = statistics.mean(dom)
-    dom_bytes = 12288 * 4096 * args.K // 8
+    # launch durations from HIP events on the launch stream: one graph holding a
+    # launch for every weight copy (distinct weights back to back), events around its
+    # replays; average = elapsed / launches
+    reps = max(1, args.steps // copies)
+
+    def per_launch_us(fn_for_copy):
+        g = capture(lambda: [fn_for_copy(c) for c in range(copies)])
+        g.replay()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / (reps * copies)
+
+    us_layer = {name: round(per_launch_us(lambda c, name=name: single(c, name)), 3)
+                for name, _, _ in LAYERS}
+    us_group = {gname: round(per_launch_us(lambda c, gname=gname: step(c, gname)), 3)
+                for gname, _ in GROUPS}
+    dom_us = us_group[DOMINANT]
+    dom_bytes = 2 * 12288 * 4096 * args.K // 8
     achieved = dom_bytes / (dom_us * 1e-6) / 1e9
     gbs = block_bytes / sec_per_step / 1e9
 
@@ -194,11 +230,14 @@ def main():
                    "rotated_bytes": block_bytes * copies,
                    "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
                    "us_per_block": round(sec_per_step * 1e6, 2),
-                   "us_per_layer": us_layer},
+                   "launches_per_block": [g for g, _ in GROUPS],
+                   "us_per_group_launch": us_group,
+                   "us_per_layer_single_launch": us_layer},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": None,
-                     "kernel": "gemv_kernel<K=3,MCG,NB=1> on gate/up/down 12288x4096",
+                     "kernel": "gemv_group_kernel<K=3,MCG,NB=1> on the gate+up group "
+                               "(2 x 12288x4096)",
                      "avg_launch_us": round(dom_us, 3),
                      "algorithmic_bytes_per_launch": dom_bytes},
     }

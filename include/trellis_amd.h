@@ -53,7 +53,8 @@ typedef enum trellis_status {
   TRELLIS_ERR_WORKSPACE = 10,  /* workspace missing or smaller than trellis_workspace_bytes */
   TRELLIS_ERR_BATCH = 11,      /* batch < 1 */
   TRELLIS_ERR_RANGE = 12,      /* tile range outside the matrix */
-  TRELLIS_ERR_LAUNCH = 13      /* the HIP runtime rejected a launch */
+  TRELLIS_ERR_LAUNCH = 13,     /* the HIP runtime rejected a launch */
+  TRELLIS_ERR_GROUP = 14       /* group of 0 or more than 8 linears, or mixed K / codebook */
 } trellis_status;
 
 /* One packed trellis linear as the loader record holds it (web/packed.js:53-62,
@@ -88,6 +89,19 @@ int trellis_workspace_bytes(const trellis_desc *W, int batch, size_t *bytes);
 int trellis_packed_linear(const trellis_desc *W, const void *x, int64_t ldx, int batch,
                           int x_dtype, void *y, int64_t ldy, int y_dtype, void *workspace,
                           size_t ws_bytes, void *stream);
+
+/* Several independent packed linears in ONE launch (no reference counterpart: the
+ * reference dispatches every linear separately, web/model.js:80-100). Intended for the
+ * linears of a decoder block that share an input (q/k/v, gate/up) or any set whose
+ * inputs are ready together. Up to 8 linears, all with the same K and codebook; each
+ * has its own x[i] (row stride ldx[i]) and y[i] (row stride ldy[i]). Same semantics per
+ * linear as trellis_packed_linear. */
+int trellis_workspace_bytes_group(const trellis_desc *const *W, int count, int batch,
+                                  size_t *bytes);
+int trellis_packed_linear_group(const trellis_desc *const *W, int count, const void *const *x,
+                                const int64_t *ldx, int batch, int x_dtype, void *const *y,
+                                const int64_t *ldy, int y_dtype, void *workspace,
+                                size_t ws_bytes, void *stream);
 
 /* Decode z-space tiles [tile_begin, tile_begin+ntiles) to fp32, 256 values per tile in
  * tile order t = (row%16)*16 + col%16. The bit-exact probe of the decode: restates

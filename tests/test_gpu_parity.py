@@ -173,3 +173,31 @@ def test_qwen3_8b_shapes_sampled_blocks(te, gpu_device, name, n, k):
     lhs = lin(0.75 * x1 - 1.5 * x2)
     rhs = 0.75 * lin(x1) - 1.5 * lin(x2)
     assert (lhs - rhs).abs().max().item() / rhs.abs().max().item() < TOL
+
+
+@pytest.mark.parametrize("batch", [1, 2, 5])
+def test_group_matches_single_and_oracle(te, gpu_device, batch):
+    """One grouped launch of q/k/v-like and odd-shaped members equals the oracle per
+    member and the single-matrix calls bit for bit."""
+    _say(f"[group] batch={batch}")
+    shapes = [(512, 1024), (128, 1024), (128, 1024), (1536, 576), (256, 336)]
+    members = []
+    for i, (n, k) in enumerate(shapes):
+        bits, rec = tn.synthetic_record(n, k, 3, seed=40 + i)
+        members.append((bits, rec, make_linear(te, bits, rec, gpu_device)))
+    grp = te.PackedGroup([m[2] for m in members])
+    rng = np.random.default_rng(batch)
+    xs = [torch.from_numpy(rng.standard_normal((batch, rec.k)).astype(np.float16)).to(gpu_device)
+          for _, rec, _ in members]
+    ys = grp(xs)
+    for (bits, rec, lin), x, y in zip(members, xs, ys):
+        want = tn.packed_linear_ref(bits, rec, x.cpu().numpy())
+        assert tn.rel_err(y.cpu().numpy(), want) < TOL
+        assert torch.equal(lin(x), y)
+
+
+def test_group_rejects_mixed_k(te, gpu_device):
+    b3, r3 = tn.synthetic_record(128, 256, 3, seed=1)
+    b2, r2 = tn.synthetic_record(128, 256, 2, seed=2)
+    with pytest.raises(ValueError):
+        te.PackedGroup([make_linear(te, b3, r3, gpu_device), make_linear(te, b2, r2, gpu_device)])

@@ -12,7 +12,8 @@ from ._capi import TrellisError, TrellisLibraryMissing
 from .format import PackedRecord, fit_block, read_packed, write_packed
 
 __all__ = ["PackedRecord", "read_packed", "write_packed", "fit_block", "TrellisError",
-           "TrellisLibraryMissing", "PackedLinear", "PackedOps", "load_packed", "library"]
+           "TrellisLibraryMissing", "PackedLinear", "PackedGroup", "PackedOps", "load_packed",
+           "library"]
 
 
 def library():
@@ -22,7 +23,7 @@ def library():
 
 def __getattr__(name):
     # torch-dependent pieces load lazily so the format tools import without torch
-    if name in ("PackedLinear", "PackedOps", "load_packed"):
+    if name in ("PackedLinear", "PackedGroup", "PackedOps", "load_packed"):
         from . import packed_linear
         return getattr(packed_linear, name)
     raise AttributeError(name)

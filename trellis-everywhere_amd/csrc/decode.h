@@ -14,13 +14,11 @@
 // a = ((240-16r)*K) >> 5) and every window's word pair and shift is a compile-time
 // constant once K and the row parity PAR are fixed.
 //
-// Codebook arithmetic (qtip.py:32-53) is done without the quarter-rate 32-bit
-// multiply: for a 16-bit state u and constant C = Chi:Clo,
-//     u*C + A mod 2^32 = u*Clo + ((u*Chi + Ahi) mod 2^16) << 16 + Alo
-// which is one v_pk_mul_lo_u16 / v_pk_mad_u16 (the high half only) and one
-// v_mad_u32_u16 (which reads only the low or, with op_sel, high 16 bits of the window
-// register, so no masking is needed). The lop3 mask/xor is one v_bitop3_b32; its result
-// is the fp16 pair (hi, lo) whose fp32 sum is the codebook value.
+// Codebook arithmetic (qtip.py:32-53) uses the full-rate gfx950 v_mul_lo_u32 on the
+// masked 16-bit state, then one v_bitop3_b32 for the lop3 mask/xor; its result is the
+// fp16 pair (hi, lo) whose fp32 sum is the codebook value. Window extraction: the row's
+// words are re-sliced at 16-bit granularity (W0, W0:W1>>16, W1, W1:W2>>16, W2), so every
+// window lies inside one 32-bit register and costs one v_bfe_u32.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -43,32 +41,10 @@ template <> struct Lcg<CB_1MAD> {
   static constexpr uint32_t MUL = 34038481u, ADD = 76625530u;
 };
 
-// P = state*MUL + ADD mod 2^32, state = low (HI=0) or high (HI=1) 16 bits of u.
-template <int CB, int HI>
-__device__ __forceinline__ uint32_t lcg_p(uint32_t u) {
-  constexpr uint32_t MUL = Lcg<CB>::MUL, ADD = Lcg<CB>::ADD;
-  constexpr uint32_t CHI_HI = MUL & 0xFFFF0000u;  // Chi in the high half, 0 in the low
-  constexpr uint32_t CLO = MUL & 0xFFFFu;
-  uint32_t t, p;
-  if constexpr (ADD == 0u) {
-    // t = [lo16(u*Chi) | 0]
-    if constexpr (HI)
-      asm("v_pk_mul_lo_u16 %0, %1, %2 op_sel:[1,0] op_sel_hi:[1,1]" : "=v"(t) : "v"(u), "s"(CHI_HI));
-    else
-      asm("v_pk_mul_lo_u16 %0, %1, %2 op_sel_hi:[0,1]" : "=v"(t) : "v"(u), "s"(CHI_HI));
-  } else {
-    // t = [lo16(u*Chi + Ahi) | Alo]
-    if constexpr (HI)
-      asm("v_pk_mad_u16 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,1,1]"
-          : "=v"(t) : "v"(u), "s"(CHI_HI), "v"(ADD));
-    else
-      asm("v_pk_mad_u16 %0, %1, %2, %3 op_sel_hi:[0,1,1]" : "=v"(t) : "v"(u), "s"(CHI_HI), "v"(ADD));
-  }
-  if constexpr (HI)
-    asm("v_mad_u32_u16 %0, %1, %2, %3 op_sel:[1,0,0,0]" : "=v"(p) : "v"(u), "s"(CLO), "v"(t));
-  else
-    asm("v_mad_u32_u16 %0, %1, %2, %3" : "=v"(p) : "v"(u), "s"(CLO), "v"(t));
-  return p;
+// P = state*MUL + ADD mod 2^32 for a 16-bit state (upper bits of `state` are zero).
+template <int CB>
+__device__ __forceinline__ uint32_t lcg_p(uint32_t state) {
+  return state * Lcg<CB>::MUL + Lcg<CB>::ADD;
 }
 
 // (P & 0x8FFF8FFF) ^ 0x3B603B60: the fp16 pair (hi, lo) of MCG / 3INST (qtip.py:44,52).
@@ -95,9 +71,9 @@ __device__ __forceinline__ float cb_exact(uint32_t raw) {
 }
 
 // Raw per-state output: the fp16 pair for MCG/3INST, the byte sum for 1MAD.
-template <int CB, int HI>
-__device__ __forceinline__ uint32_t cb_raw(uint32_t u) {
-  uint32_t p = lcg_p<CB, HI>(u);
+template <int CB>
+__device__ __forceinline__ uint32_t cb_raw(uint32_t state) {
+  const uint32_t p = lcg_p<CB>(state);
   if constexpr (CB == CB_1MAD)
     return byte_sum(p);
   else
@@ -127,22 +103,17 @@ constexpr bool row_needs_w2() {
 template <int K, int PAR, int CB, typename F>
 __device__ __forceinline__ void decode_row(uint32_t W0, uint32_t W1, uint32_t W2, F&& f) {
   constexpr int B0 = row_bit0<K, PAR>();
+  // 16-bit-aligned views of the row's 96-bit span: R[j] = bits [16j, 16j+32)
+  const uint32_t R1 = __builtin_amdgcn_alignbit(W1, W0, 16);
+  const uint32_t R3 = __builtin_amdgcn_alignbit(W2, W1, 16);
 #pragma unroll
   for (int c = 0; c < 16; ++c) {
     const int off = B0 + K * (15 - c);
-    const int pair = off >> 5;
-    const int sh = off & 31;
-    const uint32_t lo = pair == 0 ? W0 : W1;
-    const uint32_t hi = pair == 0 ? W1 : W2;
-    uint32_t raw;
-    if (sh == 0) {
-      raw = cb_raw<CB, 0>(lo);
-    } else if (sh == 16) {
-      raw = cb_raw<CB, 1>(lo);
-    } else {
-      raw = cb_raw<CB, 0>(__builtin_amdgcn_alignbit(hi, lo, sh));
-    }
-    f(c, raw);
+    const int j = off >> 4;
+    const int s = off & 15;
+    const uint32_t Rj = j == 0 ? W0 : j == 1 ? R1 : j == 2 ? W1 : j == 3 ? R3 : W2;
+    const uint32_t state = (Rj >> s) & 0xFFFFu;
+    f(c, cb_raw<CB>(state));
   }
 }
 

@@ -7,7 +7,7 @@
 
 #include "trellis_amd.h"
 #include "decode.h"
-#include "gemv.h"
+#include "gemv_launch.h"
 
 using namespace trellis;
 
@@ -76,82 +76,71 @@ int validate_fold(const trellis_desc* W) {
 
 // ---------------------------------------------------------------- GEMV plan
 constexpr int GEMV_MAX_NB = 8;
-constexpr int GEMV_MAX_KS = 64;
-
-struct GemvPlan {
-  int nb;     // batch rows per launch (1, 2, 4, 8)
-  int kS;     // tile columns per workgroup
-  int S;      // k-slices
-  int n_ob;   // 128-row output blocks
-  size_t ws;  // workspace bytes
-};
 
 int env_int(const char* name, int dflt) {
   const char* s = std::getenv(name);
   return s ? std::atoi(s) : dflt;
 }
 
-int pick_ks(int n_ob, int tiles_in, int block_in) {
-  const int forced = env_int("TRELLIS_GEMV_KS", 0);
-  const int target_wg = env_int("TRELLIS_GEMV_TARGET_WG", 1024);
-  int best = -1;
-  // valid kS: divides tiles_in, slice holds whole Hadamard blocks, fits LDS
-  for (int ks = 1; ks <= GEMV_MAX_KS && ks <= tiles_in; ++ks) {
-    if (tiles_in % ks || (ks * 16) % block_in) continue;
-    if (forced > 0 && ks == forced) return ks;
-    const int wg = n_ob * (tiles_in / ks);
-    if (wg >= target_wg || best < 0) best = ks;  // largest kS that still meets the target
-  }
-  return best;
-}
+struct GroupPlan {
+  int nb;              // batch rows per launch (1, 2, 4, 8)
+  int tpw;             // tiles per wave: a work item covers kS = 2*tpw tile columns
+  int total;           // work items over the group
+  int n_ob[GEMV_MAX_GROUP], S[GEMV_MAX_GROUP];
+  size_t ws_off[GEMV_MAX_GROUP];  // workspace offset of matrix i (tickets, then partials)
+  size_t ws;           // workspace bytes
+};
 
-GemvPlan gemv_plan(const trellis_desc* W, int batch) {
-  GemvPlan p;
+// A work item is one 128-row output block x one k-slice of 2*tpw tile columns. tpw = 8
+// unless the group has too few items to occupy every CU several times over;
+// TRELLIS_GEMV_TPW forces 4 or 8.
+GroupPlan group_plan(const trellis_desc* const* W, int count, int batch) {
+  GroupPlan p;
   const int b = batch < GEMV_MAX_NB ? batch : GEMV_MAX_NB;
   p.nb = b <= 1 ? 1 : b <= 2 ? 2 : b <= 4 ? 4 : 8;
-  p.n_ob = (W->n_out + 127) / 128;
-  const int tiles_in = W->k_in / 16;
-  p.kS = pick_ks(p.n_ob, tiles_in, W->block_in);
-  p.S = tiles_in / p.kS;
+  auto items = [&](int tpw) {
+    long long t = 0;
+    for (int i = 0; i < count; ++i)
+      t += static_cast<long long>((W[i]->n_out + 127) / 128) *
+           ((W[i]->k_in / 16 + 2 * tpw - 1) / (2 * tpw));
+    return t;
+  };
+  const int forced = env_int("TRELLIS_GEMV_TPW", 0);
+  p.tpw = forced == 4 || forced == 8 ? forced : (items(8) >= 2048 ? 8 : 4);
+  p.total = 0;
   p.ws = 0;
-  if (p.S > 1) {
-    const size_t tickets = (static_cast<size_t>(p.n_ob) * 4 + 255) & ~static_cast<size_t>(255);
-    p.ws = tickets + static_cast<size_t>(p.n_ob) * p.S * p.nb * 128 * sizeof(float);
+  for (int i = 0; i < count; ++i) {
+    p.n_ob[i] = (W[i]->n_out + 127) / 128;
+    p.S[i] = (W[i]->k_in / 16 + 2 * p.tpw - 1) / (2 * p.tpw);
+    p.total += p.n_ob[i] * p.S[i];
+    p.ws_off[i] = p.ws;
+    if (p.S[i] > 1) {
+      const size_t tickets = (static_cast<size_t>(p.n_ob[i]) * 4 + 255) & ~static_cast<size_t>(255);
+      p.ws += tickets + static_cast<size_t>(p.n_ob[i]) * p.S[i] * p.nb * 128 * sizeof(float);
+    }
   }
   return p;
 }
 
-size_t gemv_lds_bytes(int nb, int kS) {
-  return static_cast<size_t>(nb) * kS * 16 * 4 + 3 * static_cast<size_t>(nb) * 128 * 4;
-}
-
-template <int K, int CB>
-int launch_gemv_nb(int nb, const GemvArgs& a, int grid, size_t lds, hipStream_t st) {
-  switch (nb) {
-    case 1: hipLaunchKernelGGL((gemv_kernel<K, CB, 1>), dim3(grid), dim3(256), lds, st, a); break;
-    case 2: hipLaunchKernelGGL((gemv_kernel<K, CB, 2>), dim3(grid), dim3(256), lds, st, a); break;
-    case 4: hipLaunchKernelGGL((gemv_kernel<K, CB, 4>), dim3(grid), dim3(256), lds, st, a); break;
-    default: hipLaunchKernelGGL((gemv_kernel<K, CB, 8>), dim3(grid), dim3(256), lds, st, a); break;
-  }
-  return hipGetLastError() == hipSuccess ? TRELLIS_OK : TRELLIS_ERR_LAUNCH;
-}
-
-template <int K>
-int launch_gemv_k(int cb, int nb, const GemvArgs& a, int grid, size_t lds, hipStream_t st) {
-  switch (cb) {
-    case CB_MCG: return launch_gemv_nb<K, CB_MCG>(nb, a, grid, lds, st);
-    case CB_3INST: return launch_gemv_nb<K, CB_3INST>(nb, a, grid, lds, st);
-    default: return launch_gemv_nb<K, CB_1MAD>(nb, a, grid, lds, st);
+int launch_gemv(int K, int cb, int nb, int tpw, const GemvGroupArgs& g, hipStream_t st) {
+  switch (K) {
+    case 2: return launch_gemv_k<2>(cb, nb, tpw, g, st);
+    case 3: return launch_gemv_k<3>(cb, nb, tpw, g, st);
+    default: return launch_gemv_k<4>(cb, nb, tpw, g, st);
   }
 }
 
-int launch_gemv(const trellis_desc* W, int cb, int nb, const GemvArgs& a, int grid, size_t lds,
-                hipStream_t st) {
-  switch (W->K) {
-    case 2: return launch_gemv_k<2>(cb, nb, a, grid, lds, st);
-    case 3: return launch_gemv_k<3>(cb, nb, a, grid, lds, st);
-    default: return launch_gemv_k<4>(cb, nb, a, grid, lds, st);
+int validate_group(const trellis_desc* const* W, int count) {
+  if (!W || count < 1) return TRELLIS_ERR_NULL;
+  if (count > GEMV_MAX_GROUP) return TRELLIS_ERR_GROUP;
+  for (int i = 0; i < count; ++i) {
+    int v = validate(W[i]);
+    if (v) return v;
+    v = validate_fold(W[i]);
+    if (v) return v;
+    if (W[i]->K != W[0]->K || W[i]->codebook != W[0]->codebook) return TRELLIS_ERR_GROUP;
   }
+  return TRELLIS_OK;
 }
 
 template <int K>
@@ -195,8 +184,19 @@ const char* trellis_strerror(int status) {
     case TRELLIS_ERR_BATCH: return "batch must be >= 1";
     case TRELLIS_ERR_RANGE: return "tile range outside the matrix";
     case TRELLIS_ERR_LAUNCH: return "HIP kernel launch failed";
+    case TRELLIS_ERR_GROUP: return "a group holds 1..8 linears sharing K and codebook";
     default: return "unknown trellis status";
   }
+}
+
+int trellis_workspace_bytes_group(const trellis_desc* const* W, int count, int batch,
+                                  size_t* bytes) {
+  if (!bytes) return TRELLIS_ERR_NULL;
+  const int v = validate_group(W, count);
+  if (v) return v;
+  if (batch < 1) return TRELLIS_ERR_BATCH;
+  *bytes = group_plan(W, count, batch).ws;
+  return TRELLIS_OK;
 }
 
 int trellis_workspace_bytes(const trellis_desc* W, int batch, size_t* bytes) {
@@ -204,7 +204,7 @@ int trellis_workspace_bytes(const trellis_desc* W, int batch, size_t* bytes) {
   const int v = validate(W);
   if (v) return v;
   if (batch < 1) return TRELLIS_ERR_BATCH;
-  *bytes = gemv_plan(W, batch).ws;
+  *bytes = group_plan(&W, 1, batch).ws;
   return TRELLIS_OK;
 }
 
@@ -224,55 +224,79 @@ int trellis_decode_tiles(const trellis_desc* W, uint32_t tile_begin, uint32_t nt
   }
 }
 
-int trellis_packed_linear(const trellis_desc* W, const void* x, int64_t ldx, int batch,
-                          int x_dtype, void* y, int64_t ldy, int y_dtype, void* workspace,
-                          size_t ws_bytes, void* stream) {
-  int v = validate(W);
+int trellis_packed_linear_group(const trellis_desc* const* W, int count, const void* const* x,
+                                 const int64_t* ldx, int batch, int x_dtype, void* const* y,
+                                 const int64_t* ldy, int y_dtype, void* workspace,
+                                 size_t ws_bytes, void* stream) {
+  int v = validate_group(W, count);
   if (v) return v;
-  v = validate_fold(W);
-  if (v) return v;
-  if (!x || !y) return TRELLIS_ERR_NULL;
+  if (!x || !y || !ldx || !ldy) return TRELLIS_ERR_NULL;
   if (batch < 1) return TRELLIS_ERR_BATCH;
   if ((x_dtype != TRELLIS_F32 && x_dtype != TRELLIS_F16) ||
       (y_dtype != TRELLIS_F32 && y_dtype != TRELLIS_F16))
     return TRELLIS_ERR_DTYPE;
-  if (batch > 1 && (ldx < W->k_in || ldy < W->n_out)) return TRELLIS_ERR_ALIGN;
-  const GemvPlan p = gemv_plan(W, batch);
+  for (int i = 0; i < count; ++i) {
+    if (!x[i] || !y[i]) return TRELLIS_ERR_NULL;
+    if (batch > 1 && (ldx[i] < W[i]->k_in || ldy[i] < W[i]->n_out)) return TRELLIS_ERR_ALIGN;
+    // activations are read as aligned u32 words
+    if (reinterpret_cast<uintptr_t>(x[i]) % 4) return TRELLIS_ERR_ALIGN;
+    if (x_dtype == TRELLIS_F16 && batch > 1 && ldx[i] % 2) return TRELLIS_ERR_ALIGN;
+  }
+  const GroupPlan p = group_plan(W, count, batch);
   if (p.ws > 0 && (!workspace || ws_bytes < p.ws)) return TRELLIS_ERR_WORKSPACE;
   hipStream_t st = static_cast<hipStream_t>(stream);
 
-  GemvArgs a;
-  a.bits = W->bits;
-  a.su = W->su;
-  a.sv = W->sv;
-  a.isc = W->isc_scaled;
-  a.osc = W->osc;
-  a.ldx = ldx;
-  a.ldy = ldy;
-  a.n = W->n_out;
-  a.k = W->k_in;
-  a.nwords = W->nwords;
-  a.tiles_in = W->k_in / 16;
-  a.kS = p.kS;
-  a.S = p.S;
-  a.block_in = W->block_in;
-  a.block_out = W->block_out;
-  a.x_f16 = x_dtype == TRELLIS_F16;
-  a.y_f16 = y_dtype == TRELLIS_F16;
-  const size_t tickets = (static_cast<size_t>(p.n_ob) * 4 + 255) & ~static_cast<size_t>(255);
-  a.tickets = p.S > 1 ? static_cast<unsigned*>(workspace) : nullptr;
-  a.part = p.S > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + tickets) : nullptr;
-  const size_t xes = a.x_f16 ? 2 : 4, yes = a.y_f16 ? 2 : 4;
-  const size_t lds = gemv_lds_bytes(p.nb, p.kS);
-  const int grid = p.n_ob * p.S;
+  GemvGroupArgs g;
+  std::memset(&g, 0, sizeof(g));
+  g.nmat = count;
+  g.total = p.total;
+  g.nwords = W[0]->nwords;
+  g.x_f16 = x_dtype == TRELLIS_F16;
+  g.y_f16 = y_dtype == TRELLIS_F16;
+  int item0 = 0;
+  for (int i = 0; i < count; ++i) {
+    GemvMat& m = g.m[i];
+    m.bits = W[i]->bits;
+    m.su = W[i]->su;
+    m.sv = W[i]->sv;
+    m.isc = W[i]->isc_scaled;
+    m.osc = W[i]->osc;
+    m.ldx = ldx[i];
+    m.ldy = ldy[i];
+    m.n = W[i]->n_out;
+    m.k = W[i]->k_in;
+    m.tiles_in = W[i]->k_in / 16;
+    m.block_in = W[i]->block_in;
+    m.block_out = W[i]->block_out;
+    m.n_ob = p.n_ob[i];
+    m.S = p.S[i];
+    m.item0 = item0;
+    item0 += p.n_ob[i] * p.S[i];
+    if (p.S[i] > 1) {
+      char* base = static_cast<char*>(workspace) + p.ws_off[i];
+      const size_t tickets = (static_cast<size_t>(p.n_ob[i]) * 4 + 255) & ~static_cast<size_t>(255);
+      m.tickets = reinterpret_cast<unsigned*>(base);
+      m.part = reinterpret_cast<float*>(base + tickets);
+    }
+  }
+  const size_t xes = g.x_f16 ? 2 : 4, yes = g.y_f16 ? 2 : 4;
   for (int b0 = 0; b0 < batch; b0 += p.nb) {
-    a.batch = batch - b0 < p.nb ? batch - b0 : p.nb;
-    a.x = static_cast<const char*>(x) + static_cast<size_t>(b0) * ldx * xes;
-    a.y = static_cast<char*>(y) + static_cast<size_t>(b0) * ldy * yes;
-    v = launch_gemv(W, W->codebook, p.nb, a, grid, lds, st);
+    g.batch = batch - b0 < p.nb ? batch - b0 : p.nb;
+    for (int i = 0; i < count; ++i) {
+      g.m[i].x = static_cast<const char*>(x[i]) + static_cast<size_t>(b0) * ldx[i] * xes;
+      g.m[i].y = static_cast<char*>(y[i]) + static_cast<size_t>(b0) * ldy[i] * yes;
+    }
+    v = launch_gemv(W[0]->K, W[0]->codebook, p.nb, p.tpw, g, st);
     if (v) return v;
   }
   return TRELLIS_OK;
+}
+
+int trellis_packed_linear(const trellis_desc* W, const void* x, int64_t ldx, int batch,
+                          int x_dtype, void* y, int64_t ldy, int y_dtype, void* workspace,
+                          size_t ws_bytes, void* stream) {
+  return trellis_packed_linear_group(&W, 1, &x, &ldx, batch, x_dtype, &y, &ldy, y_dtype,
+                                     workspace, ws_bytes, stream);
 }
 
 }  // extern "C"

@@ -136,6 +136,82 @@ class PackedLinear:
         return out
 
 
+class PackedGroup:
+    """Several packed linears evaluated in ONE launch (trellis_packed_linear_group): e.g.
+    q/k/v or gate/up of a decoder block, which the reference dispatches one by one
+    (web/model.js:80-100). All members share K, codebook and device."""
+
+    def __init__(self, linears):
+        linears = list(linears)
+        if not 1 <= len(linears) <= 8:
+            raise ValueError("a group holds 1..8 linears")
+        dev = linears[0].device
+        for lin in linears:
+            if lin.device != dev or lin.K != linears[0].K or lin.codebook != linears[0].codebook:
+                raise ValueError("group members must share device, K and codebook")
+        self.linears = linears
+        self.device = dev
+        n = len(linears)
+        self._descs = (_capi.TrellisDesc * n)(*[lin.desc for lin in linears])
+        self._dptrs = (ctypes.POINTER(_capi.TrellisDesc) * n)(
+            *[ctypes.pointer(self._descs[i]) for i in range(n)])
+        self._ws = None
+
+    def workspace_bytes(self, batch: int) -> int:
+        lib = _capi.load()
+        nbytes = ctypes.c_size_t(0)
+        _capi.check(lib.trellis_workspace_bytes_group(self._dptrs, len(self.linears), int(batch),
+                                                      ctypes.byref(nbytes)))
+        return int(nbytes.value)
+
+    def _workspace(self, batch: int) -> torch.Tensor:
+        need = self.workspace_bytes(batch)
+        if self._ws is None or self._ws.numel() < need:
+            self._ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=self.device)
+        return self._ws
+
+    def forward(self, xs, outs=None, out_dtype: torch.dtype = torch.float32):
+        """xs: one activation per member ([k_i] or [batch, k_i], same batch and dtype);
+        returns (or fills) one output per member."""
+        lib = _capi.load()
+        n = len(self.linears)
+        if len(xs) != n:
+            raise ValueError(f"expected {n} inputs")
+        squeeze = xs[0].dim() == 1
+        x2 = [x.unsqueeze(0) if x.dim() == 1 else x for x in xs]
+        x2 = [x if x.stride(1) == 1 else x.contiguous() for x in x2]
+        B = x2[0].shape[0]
+        dt = x2[0].dtype
+        for lin, x in zip(self.linears, x2):
+            if x.shape != (B, lin.k_in) or x.dtype != dt or x.device != self.device:
+                raise ValueError("inputs must share batch, dtype and device and match k_in")
+        if dt not in (torch.float16, torch.float32):
+            raise ValueError(f"x dtype {dt} not supported")
+        if outs is None:
+            outs = [torch.empty((B, lin.n_out), dtype=out_dtype, device=self.device)
+                    for lin in self.linears]
+        y2 = [o.view(B, lin.n_out) if o.dim() == 1 else o for o, lin in zip(outs, self.linears)]
+        ydt = y2[0].dtype
+        if any(y.dtype != ydt or y.stride(1) != 1 for y in y2) or ydt not in (torch.float16,
+                                                                               torch.float32):
+            raise ValueError("outputs must share an fp16/fp32 dtype with unit column stride")
+        ws = self._workspace(B)
+        xp = (ctypes.c_void_p * n)(*[x.data_ptr() for x in x2])
+        yp = (ctypes.c_void_p * n)(*[y.data_ptr() for y in y2])
+        ldx = (ctypes.c_int64 * n)(*[x.stride(0) for x in x2])
+        ldy = (ctypes.c_int64 * n)(*[y.stride(0) for y in y2])
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        _capi.check(lib.trellis_packed_linear_group(
+            self._dptrs, n, xp, ldx, B, _capi.DT_F16 if dt == torch.float16 else _capi.DT_F32,
+            yp, ldy, _capi.DT_F16 if ydt == torch.float16 else _capi.DT_F32,
+            _ptr(ws), ws.numel(), ctypes.c_void_p(stream)))
+        if squeeze:
+            return [o[0] if o.dim() == 2 else o for o in outs]
+        return outs
+
+    __call__ = forward
+
+
 class PackedOps:
     """Mirror of the reference's PackedOps (web/packed.js:130-184): linear(W, x)
     returns {"y": y, "scale": W.scale}."""
