@@ -13,8 +13,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libtrellis_amd.so")
-SOURCES = ["trellis_amd.hip", "gemv_k2.hip", "gemv_k3.hip", "gemv_k4.hip"]
-HEADERS = ["decode.h", "gemv.h", "gemv_launch.h"]
+SOURCES = ["trellis_amd.hip", "tmk_k2.hip", "tmk_k3.hip", "tmk_k4.hip"]
+HEADERS = ["decode.h", "tmk.h", "tmk_launch.h"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"

@@ -7,18 +7,9 @@
 // word granularity (web/kernels.js:115-122); this equals qtip.py decode_window over the
 // tail-biting stream (qtip.py:82-110).
 //
-// One tile row r (t = 16r + c, c = 0..15) occupies a 16*K-1+16 bit span starting at bit
-// (240-16r)*K. For K = 2 and 4 that start is word aligned; for K = 3 it is at bit 16
-// of its first word for even r and bit 0 for odd r. decode_row<K, PAR> therefore works
-// on three consecutive words W0..W2 (word indices a, a+1, a+2 mod nwords, with
-// a = ((240-16r)*K) >> 5) and every window's word pair and shift is a compile-time
-// constant once K and the row parity PAR are fixed.
-//
 // Codebook arithmetic (qtip.py:32-53) uses the full-rate gfx950 v_mul_lo_u32 on the
 // masked 16-bit state, then one v_bitop3_b32 for the lop3 mask/xor; its result is the
-// fp16 pair (hi, lo) whose fp32 sum is the codebook value. Window extraction: the row's
-// words are re-sliced at 16-bit granularity (W0, W0:W1>>16, W1, W1:W2>>16, W2), so every
-// window lies inside one 32-bit register and costs one v_bfe_u32.
+// fp16 pair (hi, lo) whose fp32 sum is the codebook value.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -80,41 +71,28 @@ __device__ __forceinline__ uint32_t cb_raw(uint32_t state) {
     return lop3_pair(p);
 }
 
-// Word index of the first of the three words a tile row reads.
+// The four windows t = 16r + 4g + q (q = 0..3) of one lane of a 16x16 MFMA tile (r = tile
+// row, g = column group). The lowest of them (q = 3) starts at stream bit
+// o3 = (252 - 16r - 4g) * K, and all four lie in the 32-bit funnel of words (wa, wb) at
+// shift sh: wa = o3 >> 5, wb = (wa + 1) % nwords (the stream wraps at word granularity),
+// sh = o3 & 31. Window q sits at bit K*(3-q) of the funnel.
+struct QuadPos {
+  int wa, wb, sh;
+};
+
 template <int K>
-__device__ __forceinline__ int row_word0(int r) {
-  return ((240 - 16 * r) * K) >> 5;
+__device__ __forceinline__ QuadPos quad_pos(int r, int g) {
+  constexpr int NW = 8 * K;
+  const int o3 = (252 - 16 * r - 4 * g) * K;
+  return {o3 >> 5, ((o3 >> 5) + 1) % NW, o3 & 31};
 }
 
-// Bit offset of the row's lowest window (column 15) inside word W0.
-template <int K, int PAR>
-constexpr int row_bit0() {
-  return (K == 3 && PAR == 0) ? 16 : 0;
-}
-
-// Does the row need its third word?
-template <int K, int PAR>
-constexpr bool row_needs_w2() {
-  return row_bit0<K, PAR>() + K * 15 + 16 > 64;  // span ends beyond W1
-}
-
-// Decode the 16 windows of one tile row. f(c, raw) receives column c = 0..15 and the
-// raw codebook output (cb_raw) of state t = 16r + c.
-template <int K, int PAR, int CB, typename F>
-__device__ __forceinline__ void decode_row(uint32_t W0, uint32_t W1, uint32_t W2, F&& f) {
-  constexpr int B0 = row_bit0<K, PAR>();
-  // 16-bit-aligned views of the row's 96-bit span: R[j] = bits [16j, 16j+32)
-  const uint32_t R1 = __builtin_amdgcn_alignbit(W1, W0, 16);
-  const uint32_t R3 = __builtin_amdgcn_alignbit(W2, W1, 16);
+// Raw codebook outputs (cb_raw) of the lane's four windows.
+template <int K, int CB>
+__device__ __forceinline__ void decode_quad(uint32_t wlo, uint32_t whi, int sh, uint32_t (&raw)[4]) {
+  const uint32_t u = __builtin_amdgcn_alignbit(whi, wlo, sh);
 #pragma unroll
-  for (int c = 0; c < 16; ++c) {
-    const int off = B0 + K * (15 - c);
-    const int j = off >> 4;
-    const int s = off & 15;
-    const uint32_t Rj = j == 0 ? W0 : j == 1 ? R1 : j == 2 ? W1 : j == 3 ? R3 : W2;
-    const uint32_t state = (Rj >> s) & 0xFFFFu;
-    f(c, cb_raw<CB>(state));
-  }
+  for (int q = 0; q < 4; ++q) raw[q] = cb_raw<CB>((u >> (K * (3 - q))) & 0xFFFFu);
 }
 
 }  // namespace trellis

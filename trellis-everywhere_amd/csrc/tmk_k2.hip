@@ -1,0 +1,7 @@
+// Decode-to-MFMA kernel instantiations for K=2 bits per weight.
+#define TRELLIS_TMK_INSTANTIATE
+#include "tmk_launch.h"
+
+namespace trellis {
+template int launch_tmk_k<2>(int, int, const TmkArgs&, hipStream_t);
+}  // namespace trellis

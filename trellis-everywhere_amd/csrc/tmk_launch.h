@@ -1,0 +1,44 @@
+// tmk_launch.h — host launchers of the decode-to-MFMA kernels, one translation unit per
+// K (tmk_k2.hip, tmk_k3.hip, tmk_k4.hip) so the instantiations build in parallel.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "tmk.h"
+
+namespace trellis {
+
+// tmk_kernel<K, cb, ks> over g.total items (the x fold has been launched before it).
+// Returns 0 or a trellis_status code.
+template <int K>
+int launch_tmk_k(int cb, int ks, const TmkArgs& g, hipStream_t st);
+
+#ifdef TRELLIS_TMK_INSTANTIATE
+template <int K, int CB, int XB>
+static int launch_ks(int ks, const TmkArgs& g, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>(g.total));
+  switch (ks) {
+    case 4: hipLaunchKernelGGL((tmk_kernel<K, CB, 4, XB>), grid, dim3(256), 0, st, g); break;
+    case 8: hipLaunchKernelGGL((tmk_kernel<K, CB, 8, XB>), grid, dim3(256), 0, st, g); break;
+    case 16: hipLaunchKernelGGL((tmk_kernel<K, CB, 16, XB>), grid, dim3(256), 0, st, g); break;
+    default: hipLaunchKernelGGL((tmk_kernel<K, CB, 32, XB>), grid, dim3(256), 0, st, g); break;
+  }
+  return hipGetLastError() == hipSuccess ? 0 : 13;
+}
+
+template <int K, int CB>
+static int launch_xb(int ks, const TmkArgs& g, hipStream_t st) {
+  return g.batch == 1 ? launch_ks<K, CB, 1>(ks, g, st) : launch_ks<K, CB, TMK_MAX_BATCH>(ks, g, st);
+}
+
+template <int K>
+int launch_tmk_k(int cb, int ks, const TmkArgs& g, hipStream_t st) {
+  switch (cb) {
+    case CB_MCG: return launch_xb<K, CB_MCG>(ks, g, st);
+    case CB_3INST: return launch_xb<K, CB_3INST>(ks, g, st);
+    default: return launch_xb<K, CB_1MAD>(ks, g, st);
+  }
+}
+#endif
+
+}  // namespace trellis

@@ -7,41 +7,33 @@
 
 #include "trellis_amd.h"
 #include "decode.h"
-#include "gemv_launch.h"
+#define TRELLIS_XFOLD_DEFINE
+#include "tmk_launch.h"
 
 using namespace trellis;
 
 namespace {
 
 // ---------------------------------------------------------------- decode kernel
-// One thread per tile row: the same window + codebook code the matmul kernels run,
-// storing each value's exact fp32 (the fp16 halves summed in fp32).
-template <int K, int CB, int PAR>
-__device__ __forceinline__ void decode_tile_row(const uint32_t* tp, int nw, int r, float* out) {
-  const int w0 = row_word0<K>(r);
-  const uint32_t W0 = tp[w0];
-  const uint32_t W1 = tp[(w0 + 1) % nw];
-  const uint32_t W2 = tp[(w0 + 2) % nw];
-  float v[16];
-  decode_row<K, PAR, CB>(W0, W1, W2, [&](int c, uint32_t raw) { v[c] = cb_exact<CB>(raw); });
-  float4* o = reinterpret_cast<float4*>(out);
-#pragma unroll
-  for (int q = 0; q < 4; ++q) o[q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
-}
-
+// One wave per tile, lane l = (tile row r = l%16, column group g = l/16): the same
+// decode_quad the matmul kernels run, each value stored as its exact fp32 (the fp16
+// halves summed in fp32; 1MAD divided as the reference does).
 template <int K, int CB>
 __global__ __launch_bounds__(256) void decode_tiles_kernel(const uint32_t* __restrict__ bits,
-                                                           int nw, uint32_t tile0, uint32_t ntiles,
+                                                           uint32_t tile0, uint32_t ntiles,
                                                            float* __restrict__ out) {
-  const uint32_t lt = blockIdx.x * 16u + (threadIdx.x >> 4);
-  const int r = threadIdx.x & 15;
+  const uint32_t lt = blockIdx.x * 4u + (threadIdx.x >> 6);
   if (lt >= ntiles) return;
-  const uint32_t* tp = bits + static_cast<size_t>(tile0 + lt) * nw;
-  float* o = out + static_cast<size_t>(lt) * 256 + r * 16;
-  if (r & 1)
-    decode_tile_row<K, CB, 1>(tp, nw, r, o);
-  else
-    decode_tile_row<K, CB, 0>(tp, nw, r, o);
+  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  const uint32_t* tp = bits + static_cast<size_t>(tile0 + lt) * (8 * K);
+  const QuadPos qp = quad_pos<K>(r, g);
+  uint32_t raw[4];
+  decode_quad<K, CB>(tp[qp.wa], tp[qp.wb], qp.sh, raw);
+  float v[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) v[q] = cb_exact<CB>(raw[q]);
+  *reinterpret_cast<float4*>(out + static_cast<size_t>(lt) * 256 + 16 * r + 4 * g) =
+      make_float4(v[0], v[1], v[2], v[3]);
 }
 
 // ---------------------------------------------------------------- validation
@@ -74,65 +66,87 @@ int validate_fold(const trellis_desc* W) {
   return TRELLIS_OK;
 }
 
-// ---------------------------------------------------------------- GEMV plan
-constexpr int GEMV_MAX_NB = 8;
-
+// ---------------------------------------------------------------- plan
 int env_int(const char* name, int dflt) {
   const char* s = std::getenv(name);
   return s ? std::atoi(s) : dflt;
 }
 
+size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
+
 struct GroupPlan {
-  int nb;              // batch rows per launch (1, 2, 4, 8)
-  int tpw;             // tiles per wave: a work item covers kS = 2*tpw tile columns
+  int nb;              // batch rows per launch (<= TMK_MAX_BATCH)
+  int ks;              // tile columns per work item (4, 8, 16)
   int total;           // work items over the group
-  int n_ob[GEMV_MAX_GROUP], S[GEMV_MAX_GROUP];
-  size_t ws_off[GEMV_MAX_GROUP];  // workspace offset of matrix i (tickets, then partials)
+  int folds;           // x-fold jobs over the group
+  int n_ob[TMK_MAX_GROUP], S[TMK_MAX_GROUP];
+  size_t off_tickets[TMK_MAX_GROUP], off_part[TMK_MAX_GROUP], off_xf[TMK_MAX_GROUP];
   size_t ws;           // workspace bytes
 };
 
-// A work item is one 128-row output block x one k-slice of 2*tpw tile columns. tpw = 8
-// unless the group has too few items to occupy every CU several times over;
-// TRELLIS_GEMV_TPW forces 4 or 8.
+// A work item is one 128-row output block x one k-slice of ks tile columns: the largest
+// ks in {32, 16, 8} that still gives >= 512 items (2 per CU of 256), else 8;
+// TRELLIS_TMK_KS forces 4, 8, 16 or 32.
 GroupPlan group_plan(const trellis_desc* const* W, int count, int batch) {
   GroupPlan p;
-  const int b = batch < GEMV_MAX_NB ? batch : GEMV_MAX_NB;
-  p.nb = b <= 1 ? 1 : b <= 2 ? 2 : b <= 4 ? 4 : 8;
-  auto items = [&](int tpw) {
+  p.nb = batch < TMK_MAX_BATCH ? batch : TMK_MAX_BATCH;
+  auto items = [&](int ks) {
     long long t = 0;
     for (int i = 0; i < count; ++i)
-      t += static_cast<long long>((W[i]->n_out + 127) / 128) *
-           ((W[i]->k_in / 16 + 2 * tpw - 1) / (2 * tpw));
+      t += static_cast<long long>((W[i]->n_out + 127) / 128) * ((W[i]->k_in / 16 + ks - 1) / ks);
     return t;
   };
-  const int forced = env_int("TRELLIS_GEMV_TPW", 0);
-  p.tpw = forced == 4 || forced == 8 ? forced : (items(8) >= 2048 ? 8 : 4);
+  const int forced = env_int("TRELLIS_TMK_KS", 0);
+  const int target = env_int("TRELLIS_TMK_TARGET", 512);
+  if (forced == 4 || forced == 8 || forced == 16 || forced == 32)
+    p.ks = forced;
+  else
+    p.ks = items(32) >= target ? 32 : items(16) >= target ? 16 : 8;
+  // a k-slice holds whole in-dim Hadamard blocks (the batch-1 path folds x per slice)
+  int bmax = 16;
+  for (int i = 0; i < count; ++i) bmax = W[i]->block_in > bmax ? W[i]->block_in : bmax;
+  while ((p.ks * 16) % bmax) p.ks *= 2;
   p.total = 0;
+  p.folds = 0;
   p.ws = 0;
   for (int i = 0; i < count; ++i) {
     p.n_ob[i] = (W[i]->n_out + 127) / 128;
-    p.S[i] = (W[i]->k_in / 16 + 2 * p.tpw - 1) / (2 * p.tpw);
+    p.S[i] = (W[i]->k_in / 16 + p.ks - 1) / p.ks;
     p.total += p.n_ob[i] * p.S[i];
-    p.ws_off[i] = p.ws;
+    p.folds += p.nb * ((W[i]->k_in + 127) / 128);
+    p.off_tickets[i] = p.ws;
     if (p.S[i] > 1) {
-      const size_t tickets = (static_cast<size_t>(p.n_ob[i]) * 4 + 255) & ~static_cast<size_t>(255);
-      p.ws += tickets + static_cast<size_t>(p.n_ob[i]) * p.S[i] * p.nb * 128 * sizeof(float);
+      p.ws += align256(static_cast<size_t>(p.n_ob[i]) * 4);
+      p.off_part[i] = p.ws;
+      p.ws += align256(static_cast<size_t>(p.n_ob[i]) * p.S[i] * p.nb * 128 * sizeof(float));
+    } else {
+      p.off_part[i] = p.ws;
     }
+    p.off_xf[i] = p.ws;
+    p.ws += align256(static_cast<size_t>(p.nb) * W[i]->k_in * 4);
   }
   return p;
 }
 
-int launch_gemv(int K, int cb, int nb, int tpw, const GemvGroupArgs& g, hipStream_t st) {
+// The x fold of every member, then the decode-matmul.
+int launch_tmk(int K, int cb, int ks, TmkArgs& g, int folds, hipStream_t st) {
+  if (g.batch > 1) {
+    const int items = g.total;
+    g.total = folds;
+    hipLaunchKernelGGL(xfold_kernel, dim3(static_cast<unsigned>((folds + 3) / 4)), dim3(256), 0, st, g);
+    g.total = items;
+    if (hipGetLastError() != hipSuccess) return TRELLIS_ERR_LAUNCH;
+  }
   switch (K) {
-    case 2: return launch_gemv_k<2>(cb, nb, tpw, g, st);
-    case 3: return launch_gemv_k<3>(cb, nb, tpw, g, st);
-    default: return launch_gemv_k<4>(cb, nb, tpw, g, st);
+    case 2: return launch_tmk_k<2>(cb, ks, g, st);
+    case 3: return launch_tmk_k<3>(cb, ks, g, st);
+    default: return launch_tmk_k<4>(cb, ks, g, st);
   }
 }
 
 int validate_group(const trellis_desc* const* W, int count) {
   if (!W || count < 1) return TRELLIS_ERR_NULL;
-  if (count > GEMV_MAX_GROUP) return TRELLIS_ERR_GROUP;
+  if (count > TMK_MAX_GROUP) return TRELLIS_ERR_GROUP;
   for (int i = 0; i < count; ++i) {
     int v = validate(W[i]);
     if (v) return v;
@@ -144,18 +158,18 @@ int validate_group(const trellis_desc* const* W, int count) {
 }
 
 template <int K>
-int launch_decode_k(int cb, const uint32_t* bits, int nw, uint32_t t0, uint32_t nt, float* out,
+int launch_decode_k(int cb, const uint32_t* bits, uint32_t t0, uint32_t nt, float* out,
                     hipStream_t st) {
-  const dim3 grid((nt + 15) / 16);
+  const dim3 grid((nt + 3) / 4);
   switch (cb) {
     case CB_MCG:
-      hipLaunchKernelGGL((decode_tiles_kernel<K, CB_MCG>), grid, dim3(256), 0, st, bits, nw, t0, nt, out);
+      hipLaunchKernelGGL((decode_tiles_kernel<K, CB_MCG>), grid, dim3(256), 0, st, bits, t0, nt, out);
       break;
     case CB_3INST:
-      hipLaunchKernelGGL((decode_tiles_kernel<K, CB_3INST>), grid, dim3(256), 0, st, bits, nw, t0, nt, out);
+      hipLaunchKernelGGL((decode_tiles_kernel<K, CB_3INST>), grid, dim3(256), 0, st, bits, t0, nt, out);
       break;
     default:
-      hipLaunchKernelGGL((decode_tiles_kernel<K, CB_1MAD>), grid, dim3(256), 0, st, bits, nw, t0, nt, out);
+      hipLaunchKernelGGL((decode_tiles_kernel<K, CB_1MAD>), grid, dim3(256), 0, st, bits, t0, nt, out);
       break;
   }
   return hipGetLastError() == hipSuccess ? TRELLIS_OK : TRELLIS_ERR_LAUNCH;
@@ -218,9 +232,9 @@ int trellis_decode_tiles(const trellis_desc* W, uint32_t tile_begin, uint32_t nt
   if (ntiles == 0) return TRELLIS_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (W->K) {
-    case 2: return launch_decode_k<2>(W->codebook, W->bits, W->nwords, tile_begin, ntiles, out, st);
-    case 3: return launch_decode_k<3>(W->codebook, W->bits, W->nwords, tile_begin, ntiles, out, st);
-    default: return launch_decode_k<4>(W->codebook, W->bits, W->nwords, tile_begin, ntiles, out, st);
+    case 2: return launch_decode_k<2>(W->codebook, W->bits, tile_begin, ntiles, out, st);
+    case 3: return launch_decode_k<3>(W->codebook, W->bits, tile_begin, ntiles, out, st);
+    default: return launch_decode_k<4>(W->codebook, W->bits, tile_begin, ntiles, out, st);
   }
 }
 
@@ -243,10 +257,11 @@ int trellis_packed_linear_group(const trellis_desc* const* W, int count, const v
     if (x_dtype == TRELLIS_F16 && batch > 1 && ldx[i] % 2) return TRELLIS_ERR_ALIGN;
   }
   const GroupPlan p = group_plan(W, count, batch);
-  if (p.ws > 0 && (!workspace || ws_bytes < p.ws)) return TRELLIS_ERR_WORKSPACE;
+  if (!workspace || ws_bytes < p.ws) return TRELLIS_ERR_WORKSPACE;
+  if (reinterpret_cast<uintptr_t>(workspace) % 256) return TRELLIS_ERR_ALIGN;
   hipStream_t st = static_cast<hipStream_t>(stream);
 
-  GemvGroupArgs g;
+  TmkArgs g;
   std::memset(&g, 0, sizeof(g));
   g.nmat = count;
   g.total = p.total;
@@ -254,8 +269,9 @@ int trellis_packed_linear_group(const trellis_desc* const* W, int count, const v
   g.x_f16 = x_dtype == TRELLIS_F16;
   g.y_f16 = y_dtype == TRELLIS_F16;
   int item0 = 0;
+  char* ws = static_cast<char*>(workspace);
   for (int i = 0; i < count; ++i) {
-    GemvMat& m = g.m[i];
+    TmkMat& m = g.m[i];
     m.bits = W[i]->bits;
     m.su = W[i]->su;
     m.sv = W[i]->sv;
@@ -272,21 +288,21 @@ int trellis_packed_linear_group(const trellis_desc* const* W, int count, const v
     m.S = p.S[i];
     m.item0 = item0;
     item0 += p.n_ob[i] * p.S[i];
-    if (p.S[i] > 1) {
-      char* base = static_cast<char*>(workspace) + p.ws_off[i];
-      const size_t tickets = (static_cast<size_t>(p.n_ob[i]) * 4 + 255) & ~static_cast<size_t>(255);
-      m.tickets = reinterpret_cast<unsigned*>(base);
-      m.part = reinterpret_cast<float*>(base + tickets);
-    }
+    m.tickets = reinterpret_cast<unsigned*>(ws + p.off_tickets[i]);
+    m.part = reinterpret_cast<float*>(ws + p.off_part[i]);
+    m.xf = reinterpret_cast<uint32_t*>(ws + p.off_xf[i]);
   }
   const size_t xes = g.x_f16 ? 2 : 4, yes = g.y_f16 ? 2 : 4;
   for (int b0 = 0; b0 < batch; b0 += p.nb) {
     g.batch = batch - b0 < p.nb ? batch - b0 : p.nb;
+    int chunk0 = 0;
     for (int i = 0; i < count; ++i) {
       g.m[i].x = static_cast<const char*>(x[i]) + static_cast<size_t>(b0) * ldx[i] * xes;
       g.m[i].y = static_cast<char*>(y[i]) + static_cast<size_t>(b0) * ldy[i] * yes;
+      g.m[i].chunk0 = chunk0;
+      chunk0 += g.batch * ((W[i]->k_in + 127) / 128);
     }
-    v = launch_gemv(W[0]->K, W[0]->codebook, p.nb, p.tpw, g, st);
+    v = launch_tmk(W[0]->K, W[0]->codebook, p.ks, g, chunk0, st);
     if (v) return v;
   }
   return TRELLIS_OK;
