@@ -35,6 +35,26 @@ GROUPS = [("qkv", ("q", "k", "v")), ("o", ("o",)), ("gate_up", ("gate", "up")),
           ("down", ("down",))]
 DOMINANT = "gate_up"   # 2 x 18,874,368 packed bytes per launch
 HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "tmk_gate_up_b1_traffic.txt")
+
+
+def traffic_from_profile(path=TRAFFIC_FILE):
+    """HBM bytes per gate+up launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    summary, each counter scaled by what it reads for a device copy of known size.
+    None when the summary is absent (counters cannot be read from inside this process)."""
+    if not os.path.exists(path):
+        return None
+    vals = {}
+    for line in open(path):
+        parts = line.split()
+        if len(parts) == 2 and not line.startswith("#"):
+            vals[parts[0]] = float(parts[1])
+    try:
+        fetch = vals["fetch_kib"] * vals["copy_kib"] / vals["copy_fetch_kib"]
+        write = vals["write_kib"] * vals["copy_kib"] / vals["copy_write_kib"]
+    except KeyError:
+        return None
+    return int(round((fetch + write) * 1024))
 
 
 def make_block(te, torch, dev, K, seed, codebook="mcg"):
@@ -235,9 +255,12 @@ def main():
                    "us_per_layer_single_launch": us_layer},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None,
-                     "kernel": "gemv_group_kernel<K=3,MCG,NB=1> on the gate+up group "
-                               "(2 x 12288x4096)",
+                     "traffic": traffic_from_profile() if args.batch == 1 and args.K == 3
+                     else None,
+                     "traffic_source": "profiles/tmk_gate_up_b1_traffic.txt (rocprofv3 "
+                                       "FETCH_SIZE/WRITE_SIZE, copy-scaled)",
+                     "kernel": "tmk_kernel<K=3,MCG,KS,XB=1> on the gate+up group "
+                               "(2 x 12288x4096, one launch)",
                      "avg_launch_us": round(dom_us, 3),
                      "algorithmic_bytes_per_launch": dom_bytes},
     }

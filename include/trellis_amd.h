@@ -85,7 +85,10 @@ int trellis_workspace_bytes(const trellis_desc *W, int batch, size_t *bytes);
  * (web/packed.js:163-182) and its Python mirror linear() (scripts/run_packed_headless.py:87-99).
  *   x: [batch, k_in] with row stride ldx elements, dtype x_dtype (f16 or f32)
  *   y: [batch, n_out] with row stride ldy elements, dtype y_dtype (f16 or f32)
- * Batch < 16 runs the decode-GEMV kernel; batch >= 16 the decode-to-LDS MFMA kernel. */
+ * Every batch runs the decode-to-MFMA kernel: packed words are staged in LDS with
+ * coalesced 16-byte loads, each lane decodes its part of a 16x16 tile straight into the
+ * A operand of v_mfma_f32_16x16x32_f16, and batch rows are the B columns (up to 16 per
+ * launch; larger batches run in chunks of 16 rows). */
 int trellis_packed_linear(const trellis_desc *W, const void *x, int64_t ldx, int batch,
                           int x_dtype, void *y, int64_t ldy, int y_dtype, void *workspace,
                           size_t ws_bytes, void *stream);

@@ -76,7 +76,7 @@ size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
 struct GroupPlan {
   int nb;              // batch rows per launch (<= TMK_MAX_BATCH)
-  int ks;              // tile columns per work item (4, 8, 16)
+  int ks;              // tile columns per work item (4, 8, 16, 32)
   int total;           // work items over the group
   int folds;           // x-fold jobs over the group
   int n_ob[TMK_MAX_GROUP], S[TMK_MAX_GROUP];
@@ -85,8 +85,8 @@ struct GroupPlan {
 };
 
 // A work item is one 128-row output block x one k-slice of ks tile columns: the largest
-// ks in {32, 16, 8} that still gives >= 512 items (2 per CU of 256), else 8;
-// TRELLIS_TMK_KS forces 4, 8, 16 or 32.
+// ks in {32, 16} that still gives >= 256 items (one per CU), else 8 (TRELLIS_TMK_TARGET
+// overrides the 256; TRELLIS_TMK_KS forces 4, 8, 16 or 32).
 GroupPlan group_plan(const trellis_desc* const* W, int count, int batch) {
   GroupPlan p;
   p.nb = batch < TMK_MAX_BATCH ? batch : TMK_MAX_BATCH;
@@ -97,7 +97,7 @@ GroupPlan group_plan(const trellis_desc* const* W, int count, int batch) {
     return t;
   };
   const int forced = env_int("TRELLIS_TMK_KS", 0);
-  const int target = env_int("TRELLIS_TMK_TARGET", 512);
+  const int target = env_int("TRELLIS_TMK_TARGET", 256);
   if (forced == 4 || forced == 8 || forced == 16 || forced == 32)
     p.ks = forced;
   else
