@@ -10,7 +10,8 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libtrellis_amd.so")
+# TRELLIS_AMD_LIB points the binding at another build of the same library
+LIB_PATH = os.environ.get("TRELLIS_AMD_LIB") or os.path.join(HERE, "libtrellis_amd.so")
 
 # enum trellis_codebook / trellis_dtype (include/trellis_amd.h)
 CB_IDS = {"mcg": 0, "3inst": 1, "1mad": 2}

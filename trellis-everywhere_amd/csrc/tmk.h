@@ -64,6 +64,7 @@ struct TmkArgs {
   int nwords;
   int batch;            // 1..16
   int x_f16, y_f16;
+  int kr;               // gemv_kernel: tile columns per k-range
 };
 
 // Activation i of an f16 or f32 array, read as the aligned u32 word holding it so the

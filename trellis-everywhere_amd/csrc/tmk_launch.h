@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include "gemv.h"
 #include "tmk.h"
 
 namespace trellis {
@@ -12,6 +13,10 @@ namespace trellis {
 // Returns 0 or a trellis_status code.
 template <int K>
 int launch_tmk_k(int cb, int ks, const TmkArgs& g, hipStream_t st);
+
+// gemv_kernel<K, cb, kc> over g.total items (batch 1, k-ranges of g.kr tiles).
+template <int K>
+int launch_gemv_k(int cb, int kc, const TmkArgs& g, hipStream_t st);
 
 #ifdef TRELLIS_TMK_INSTANTIATE
 template <int K, int CB, int XB>
@@ -37,6 +42,25 @@ int launch_tmk_k(int cb, int ks, const TmkArgs& g, hipStream_t st) {
     case CB_MCG: return launch_xb<K, CB_MCG>(ks, g, st);
     case CB_3INST: return launch_xb<K, CB_3INST>(ks, g, st);
     default: return launch_xb<K, CB_1MAD>(ks, g, st);
+  }
+}
+
+template <int K, int CB>
+static int launch_gemv_kc(int kc, const TmkArgs& g, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>(g.total));
+  if (kc == 8)
+    hipLaunchKernelGGL((gemv_kernel<K, CB, 8, GEMV_PF>), grid, dim3(64 * GEMV_WAVES), 0, st, g);
+  else
+    hipLaunchKernelGGL((gemv_kernel<K, CB, 16, GEMV_PF>), grid, dim3(64 * GEMV_WAVES), 0, st, g);
+  return hipGetLastError() == hipSuccess ? 0 : 13;
+}
+
+template <int K>
+int launch_gemv_k(int cb, int kc, const TmkArgs& g, hipStream_t st) {
+  switch (cb) {
+    case CB_MCG: return launch_gemv_kc<K, CB_MCG>(kc, g, st);
+    case CB_3INST: return launch_gemv_kc<K, CB_3INST>(kc, g, st);
+    default: return launch_gemv_kc<K, CB_1MAD>(kc, g, st);
   }
 }
 #endif

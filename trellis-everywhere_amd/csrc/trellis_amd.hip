@@ -76,7 +76,10 @@ size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
 struct GroupPlan {
   int nb;              // batch rows per launch (<= TMK_MAX_BATCH)
-  int ks;              // tile columns per work item (4, 8, 16, 32)
+  int gemv;            // 1: batch-1 gemv_kernel, 0: tmk_kernel
+  int kr;              // gemv: tile columns per k-range
+  int kc;              // gemv: tile columns per pipeline stage (8 or 16)
+  int ks;              // tmk: tile columns per work item (4, 8, 16, 32)
   int total;           // work items over the group
   int folds;           // x-fold jobs over the group
   int n_ob[TMK_MAX_GROUP], S[TMK_MAX_GROUP];
@@ -84,12 +87,63 @@ struct GroupPlan {
   size_t ws;           // workspace bytes
 };
 
-// A work item is one 128-row output block x one k-slice of ks tile columns: the largest
-// ks in {32, 16} that still gives >= 256 items (one per CU), else 8 (TRELLIS_TMK_TARGET
-// overrides the 256; TRELLIS_TMK_KS forces 4, 8, 16 or 32).
+int device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    cus = 256;
+  return cus;
+}
+
+// Batch 1 (gemv_kernel): a work item is one 128-row output block x one k-range of kr tile
+// columns (kr a multiple of 8, so a k-range holds whole 128-column fold chunks), run by one
+// 16-wave workgroup; one workgroup fits a CU. kr minimises an estimate of the launch time in
+// 2.4 GHz cycles: rounds of items over the CUs x the decode of 8 bands x kr/2 tiles per wave
+// at ~50 cycles per tile with four waves per SIMD, plus ~2 us of split-K epilogue (publish,
+// ticket, reduce) and ~0.1 us of ticket contention per slice when kr does not cover k, plus
+// a first-load latency for every round after the first. TRELLIS_GEMV_KR forces a value.
+int gemv_kr(const trellis_desc* const* W, int count) {
+  int maxt = 0;
+  for (int i = 0; i < count; ++i) maxt = W[i]->k_in / 16 > maxt ? W[i]->k_in / 16 : maxt;
+  const int cap = ((maxt + 7) / 8) * 8 < GEMV_MAX_KR ? ((maxt + 7) / 8) * 8 : GEMV_MAX_KR;
+  const int forced = env_int("TRELLIS_GEMV_KR", 0);
+  if (forced >= 8 && forced <= GEMV_MAX_KR && forced % 8 == 0) return forced;
+  const long long cus = device_cus();
+  int best = 8;
+  long long best_cost = -1;
+  for (int kr = 8; kr <= cap; kr += 8) {
+    long long items = 0;
+    int smax = 1;
+    for (int i = 0; i < count; ++i) {
+      const int S = (W[i]->k_in / 16 + kr - 1) / kr;
+      items += static_cast<long long>((W[i]->n_out + 127) / 128) * S;
+      smax = S > smax ? S : smax;
+    }
+    const long long rounds = (items + cus - 1) / cus;
+    const long long cost = rounds * kr * 100 + (smax > 1 ? 4800 + 240 * smax : 0) +
+                           (rounds - 1) * 3600;
+    if (best_cost < 0 || cost < best_cost) {
+      best = kr;
+      best_cost = cost;
+    }
+  }
+  return best;
+}
+
+// Batch > 1 (tmk_kernel): a work item is one 128-row output block x one k-slice of ks tile
+// columns: the largest ks in {32, 16} that still gives >= 256 items (one per CU), else 8
+// (TRELLIS_TMK_TARGET overrides the 256; TRELLIS_TMK_KS forces 4, 8, 16 or 32).
 GroupPlan group_plan(const trellis_desc* const* W, int count, int batch) {
   GroupPlan p;
   p.nb = batch < TMK_MAX_BATCH ? batch : TMK_MAX_BATCH;
+  p.gemv = batch == 1 && env_int("TRELLIS_GEMV", 1) != 0;
+  p.kr = p.gemv ? gemv_kr(W, count) : 0;
+  p.kc = p.kr >= 32 ? 16 : 8;
+  {
+    const int kc = env_int("TRELLIS_GEMV_KC", 0);
+    if ((kc == 8 || kc == 16) && kc <= p.kr) p.kc = kc;
+  }
   auto items = [&](int ks) {
     long long t = 0;
     for (int i = 0; i < count; ++i)
@@ -111,7 +165,8 @@ GroupPlan group_plan(const trellis_desc* const* W, int count, int batch) {
   p.ws = 0;
   for (int i = 0; i < count; ++i) {
     p.n_ob[i] = (W[i]->n_out + 127) / 128;
-    p.S[i] = (W[i]->k_in / 16 + p.ks - 1) / p.ks;
+    const int span = p.gemv ? p.kr : p.ks;
+    p.S[i] = (W[i]->k_in / 16 + span - 1) / span;
     p.total += p.n_ob[i] * p.S[i];
     p.folds += p.nb * ((W[i]->k_in + 127) / 128);
     p.off_tickets[i] = p.ws;
@@ -126,6 +181,15 @@ GroupPlan group_plan(const trellis_desc* const* W, int count, int batch) {
     p.ws += align256(static_cast<size_t>(p.nb) * W[i]->k_in * 4);
   }
   return p;
+}
+
+// Batch 1: the wave-pipelined decode-GEMV (its x fold is fused).
+int launch_gemv(int K, int cb, int kc, const TmkArgs& g, hipStream_t st) {
+  switch (K) {
+    case 2: return launch_gemv_k<2>(cb, kc, g, st);
+    case 3: return launch_gemv_k<3>(cb, kc, g, st);
+    default: return launch_gemv_k<4>(cb, kc, g, st);
+  }
 }
 
 // The x fold of every member, then the decode-matmul.
@@ -181,6 +245,8 @@ int launch_decode_k(int cb, const uint32_t* bits, uint32_t t0, uint32_t nt, floa
 extern "C" {
 
 const char* trellis_version(void) { return "trellis-amd 0.1 gfx950"; }
+
+
 
 const char* trellis_strerror(int status) {
   switch (status) {
@@ -268,6 +334,7 @@ int trellis_packed_linear_group(const trellis_desc* const* W, int count, const v
   g.nwords = W[0]->nwords;
   g.x_f16 = x_dtype == TRELLIS_F16;
   g.y_f16 = y_dtype == TRELLIS_F16;
+  g.kr = p.kr;
   int item0 = 0;
   char* ws = static_cast<char*>(workspace);
   for (int i = 0; i < count; ++i) {
@@ -302,7 +369,8 @@ int trellis_packed_linear_group(const trellis_desc* const* W, int count, const v
       g.m[i].chunk0 = chunk0;
       chunk0 += g.batch * ((W[i]->k_in + 127) / 128);
     }
-    v = launch_tmk(W[0]->K, W[0]->codebook, p.ks, g, chunk0, st);
+    v = p.gemv ? launch_gemv(W[0]->K, W[0]->codebook, p.kc, g, st)
+               : launch_tmk(W[0]->K, W[0]->codebook, p.ks, g, chunk0, st);
     if (v) return v;
   }
   return TRELLIS_OK;
