@@ -14,7 +14,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libtrellis_amd.so")
 SOURCES = ["trellis_amd.hip", "tmk_k2.hip", "tmk_k3.hip", "tmk_k4.hip"]
-HEADERS = ["decode.h", "tmk.h", "tmk_launch.h"]
+HEADERS = ["decode.h", "tmk.h", "gemv.h", "bgemm.h", "tmk_launch.h"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"

@@ -55,6 +55,7 @@ struct TmkMat {
   int n_ob, S;
   int item0;            // first group-wide work item of this matrix
   int chunk0;           // first group-wide x-fold job of this matrix
+  int fold0;            // first group-wide bfold_kernel workgroup of this matrix
 };
 
 struct TmkArgs {
@@ -101,6 +102,14 @@ __device__ __forceinline__ uint32_t dup_half(float v) {
   const _Float16 h = static_cast<_Float16>(v);
   const uint16_t u = __builtin_bit_cast(uint16_t, h);
   return (static_cast<uint32_t>(u) << 16) | u;
+}
+
+__device__ __forceinline__ int locate_fold(const TmkArgs& g, int it) {
+  int mi = 0;
+#pragma unroll
+  for (int j = 1; j < TMK_MAX_GROUP; ++j)
+    if (j < g.nmat && it >= g.m[j].fold0) mi = j;
+  return mi;
 }
 
 __device__ __forceinline__ int locate_mat(const TmkArgs& g, int it, bool by_chunk) {

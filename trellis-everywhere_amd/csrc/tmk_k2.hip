@@ -5,4 +5,5 @@
 namespace trellis {
 template int launch_tmk_k<2>(int, int, const TmkArgs&, hipStream_t);
 template int launch_gemv_k<2>(int, int, const TmkArgs&, hipStream_t);
+template int launch_bgemm_k<2>(int, int, const TmkArgs&, hipStream_t);
 }  // namespace trellis

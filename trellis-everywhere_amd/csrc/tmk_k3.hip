@@ -5,4 +5,5 @@
 namespace trellis {
 template int launch_tmk_k<3>(int, int, const TmkArgs&, hipStream_t);
 template int launch_gemv_k<3>(int, int, const TmkArgs&, hipStream_t);
+template int launch_bgemm_k<3>(int, int, const TmkArgs&, hipStream_t);
 }  // namespace trellis

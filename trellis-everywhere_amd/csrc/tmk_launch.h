@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include "bgemm.h"
 #include "gemv.h"
 #include "tmk.h"
 
@@ -17,6 +18,35 @@ int launch_tmk_k(int cb, int ks, const TmkArgs& g, hipStream_t st);
 // gemv_kernel<K, cb, kc> over g.total items (batch 1, k-ranges of g.kr tiles).
 template <int K>
 int launch_gemv_k(int cb, int kc, const TmkArgs& g, hipStream_t st);
+
+// bgemm_kernel<K, cb, nc> over g.total items (the x fold has been launched before it).
+template <int K>
+int launch_bgemm_k(int cb, int nc, const TmkArgs& g, hipStream_t st);
+
+// bfold_kernel<cb, nc> over nfold workgroups (after a split-K bgemm_kernel).
+int launch_bfold(int cb, int nc, int nfold, const TmkArgs& g, hipStream_t st);
+
+#ifdef TRELLIS_BFOLD_DEFINE
+template <int CB>
+static int launch_bfold_cb(int nc, int nfold, const TmkArgs& g, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>(nfold));
+  switch (nc) {
+    case 1: hipLaunchKernelGGL((bfold_kernel<CB, 1>), grid, dim3(256), 0, st, g); break;
+    case 2: hipLaunchKernelGGL((bfold_kernel<CB, 2>), grid, dim3(256), 0, st, g); break;
+    case 4: hipLaunchKernelGGL((bfold_kernel<CB, 4>), grid, dim3(256), 0, st, g); break;
+    default: hipLaunchKernelGGL((bfold_kernel<CB, 8>), grid, dim3(256), 0, st, g); break;
+  }
+  return hipGetLastError() == hipSuccess ? 0 : 13;
+}
+
+int launch_bfold(int cb, int nc, int nfold, const TmkArgs& g, hipStream_t st) {
+  switch (cb) {
+    case CB_MCG: return launch_bfold_cb<CB_MCG>(nc, nfold, g, st);
+    case CB_3INST: return launch_bfold_cb<CB_3INST>(nc, nfold, g, st);
+    default: return launch_bfold_cb<CB_1MAD>(nc, nfold, g, st);
+  }
+}
+#endif
 
 #ifdef TRELLIS_TMK_INSTANTIATE
 template <int K, int CB, int XB>
@@ -61,6 +91,27 @@ int launch_gemv_k(int cb, int kc, const TmkArgs& g, hipStream_t st) {
     case CB_MCG: return launch_gemv_kc<K, CB_MCG>(kc, g, st);
     case CB_3INST: return launch_gemv_kc<K, CB_3INST>(kc, g, st);
     default: return launch_gemv_kc<K, CB_1MAD>(kc, g, st);
+  }
+}
+
+template <int K, int CB>
+static int launch_bgemm_nc(int nc, const TmkArgs& g, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>(g.total));
+  switch (nc) {
+    case 1: hipLaunchKernelGGL((bgemm_kernel<K, CB, 1>), grid, dim3(256), 0, st, g); break;
+    case 2: hipLaunchKernelGGL((bgemm_kernel<K, CB, 2>), grid, dim3(256), 0, st, g); break;
+    case 4: hipLaunchKernelGGL((bgemm_kernel<K, CB, 4>), grid, dim3(256), 0, st, g); break;
+    default: hipLaunchKernelGGL((bgemm_kernel<K, CB, 8>), grid, dim3(256), 0, st, g); break;
+  }
+  return hipGetLastError() == hipSuccess ? 0 : 13;
+}
+
+template <int K>
+int launch_bgemm_k(int cb, int nc, const TmkArgs& g, hipStream_t st) {
+  switch (cb) {
+    case CB_MCG: return launch_bgemm_nc<K, CB_MCG>(nc, g, st);
+    case CB_3INST: return launch_bgemm_nc<K, CB_3INST>(nc, g, st);
+    default: return launch_bgemm_nc<K, CB_1MAD>(nc, g, st);
   }
 }
 #endif

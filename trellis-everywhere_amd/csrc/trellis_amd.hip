@@ -2,12 +2,14 @@
 // kernels: the bit-exact tile decode and the fused decode-GEMV.
 #include <hip/hip_runtime.h>
 
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 
 #include "trellis_amd.h"
 #include "decode.h"
 #define TRELLIS_XFOLD_DEFINE
+#define TRELLIS_BFOLD_DEFINE
 #include "tmk_launch.h"
 
 using namespace trellis;
@@ -75,9 +77,11 @@ int env_int(const char* name, int dflt) {
 size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
 struct GroupPlan {
-  int nb;              // batch rows per launch (<= TMK_MAX_BATCH)
-  int gemv;            // 1: batch-1 gemv_kernel, 0: tmk_kernel
-  int kr;              // gemv: tile columns per k-range
+  int nb;              // batch rows per launch
+  int gemv;            // batch-1 gemv_kernel
+  int tmk;             // tmk_kernel in chunks of 16 rows (TRELLIS_TMK=1)
+  int nc, ncb;         // bgemm: 16-column chunks per workgroup, column blocks
+  int kr;              // gemv / bgemm: tile columns per k-range
   int kc;              // gemv: tile columns per pipeline stage (8 or 16)
   int ks;              // tmk: tile columns per work item (4, 8, 16, 32)
   int total;           // work items over the group
@@ -134,15 +138,65 @@ int gemv_kr(const trellis_desc* const* W, int count) {
 // Batch > 1 (tmk_kernel): a work item is one 128-row output block x one k-slice of ks tile
 // columns: the largest ks in {32, 16} that still gives >= 256 items (one per CU), else 8
 // (TRELLIS_TMK_TARGET overrides the 256; TRELLIS_TMK_KS forces 4, 8, 16 or 32).
+// Batch >= 2 (bgemm_kernel): NC 16-column batch chunks per workgroup (up to 128 columns),
+// a work item is one 128-row block x one column block x one k-range of kr tile columns
+// (a multiple of the k-step, 8 tiles up to 64 columns, else 4). A workgroup has one wave
+// per SIMD, so a CU needs two or three resident workgroups to hide latency: kr minimises
+// ceil(items/CUs) x the per-wave work of an item (2 bands x kr tiles x (decode ~61 + NC
+// MFMAs x ~19 cycles)) divided by an occupancy efficiency (0.4 / 0.7 / 1 for 1 / 2 / >= 3
+// resident workgroups, the residency capped by LDS and registers), plus, with split-K, the
+// bfold_kernel launch that adds the S partial blocks and folds. At most 8 slices.
+// TRELLIS_BGEMM_KR forces a value.
+int bgemm_nc(int batch) { return batch <= 16 ? 1 : batch <= 32 ? 2 : batch <= 64 ? 4 : 8; }
+
+int bgemm_kr(const trellis_desc* const* W, int count, int batch, int nc) {
+  int maxt = 0;
+  for (int i = 0; i < count; ++i) maxt = W[i]->k_in / 16 > maxt ? W[i]->k_in / 16 : maxt;
+  const int kt = nc <= 4 ? 8 : 4;
+  const int cap = ((maxt + kt - 1) / kt) * kt;
+  const int forced = env_int("TRELLIS_BGEMM_KR", 0);
+  if (forced >= kt && forced % kt == 0) return forced < cap ? forced : cap;
+  const long long cus = device_cus();
+  const long long ncb = (batch + 16 * nc - 1) / (16 * nc);
+  int best = cap;
+  long long best_cost = -1;
+  for (int kr = kt; kr <= cap; kr += kt) {
+    long long items = 0;
+    int smax = 1;
+    for (int i = 0; i < count; ++i) {
+      const int S = (W[i]->k_in / 16 + kr - 1) / kr;
+      items += static_cast<long long>((W[i]->n_out + 127) / 128) * ncb * S;
+      smax = S > smax ? S : smax;
+    }
+    if (smax > 8) continue;
+    const long long ipc = (items + cus - 1) / cus;
+    const long long rmax = nc == 1 ? 6 : nc == 2 ? 4 : nc == 4 ? 2 : 2;
+    const long long res = ipc < rmax ? ipc : rmax;
+    const long long eff10 = res >= 3 ? 10 : res == 2 ? 7 : 4;
+    // split-K: one more launch (~1.5 us) that reads smax partial blocks of 16*nc x 128
+    // floats per (block, column block) at ~64 bytes per cycle per CU
+    const long long epi = smax > 1 ? 3600 + 1200 + smax * 16 * nc * 128 * 4 / 64 : 0;
+    const long long cost = ipc * kr * 2 * (61 + 19 * nc) * 10 / eff10 + epi;
+    if (best_cost < 0 || cost < best_cost) {
+      best = kr;
+      best_cost = cost;
+    }
+  }
+  return best;
+}
+
 GroupPlan group_plan(const trellis_desc* const* W, int count, int batch) {
   GroupPlan p;
-  p.nb = batch < TMK_MAX_BATCH ? batch : TMK_MAX_BATCH;
   p.gemv = batch == 1 && env_int("TRELLIS_GEMV", 1) != 0;
-  p.kr = p.gemv ? gemv_kr(W, count) : 0;
+  p.tmk = !p.gemv && env_int("TRELLIS_TMK", 0) != 0;
+  p.nb = p.tmk ? (batch < TMK_MAX_BATCH ? batch : TMK_MAX_BATCH) : batch;
+  p.nc = bgemm_nc(batch);
+  p.ncb = (batch + 16 * p.nc - 1) / (16 * p.nc);
+  p.kr = p.gemv ? gemv_kr(W, count) : p.tmk ? 0 : bgemm_kr(W, count, batch, p.nc);
   p.kc = p.kr >= 32 ? 16 : 8;
   {
     const int kc = env_int("TRELLIS_GEMV_KC", 0);
-    if ((kc == 8 || kc == 16) && kc <= p.kr) p.kc = kc;
+    if (p.gemv && (kc == 8 || kc == 16) && kc <= p.kr) p.kc = kc;
   }
   auto items = [&](int ks) {
     long long t = 0;
@@ -163,22 +217,25 @@ GroupPlan group_plan(const trellis_desc* const* W, int count, int batch) {
   p.total = 0;
   p.folds = 0;
   p.ws = 0;
+  const int ncb = p.gemv || p.tmk ? 1 : p.ncb;
+  const int part_cols = p.gemv ? 1 : p.tmk ? p.nb : 16 * p.nc;
   for (int i = 0; i < count; ++i) {
     p.n_ob[i] = (W[i]->n_out + 127) / 128;
-    const int span = p.gemv ? p.kr : p.ks;
+    const int span = p.tmk ? p.ks : p.kr;
     p.S[i] = (W[i]->k_in / 16 + span - 1) / span;
-    p.total += p.n_ob[i] * p.S[i];
+    p.total += p.n_ob[i] * ncb * p.S[i];
     p.folds += p.nb * ((W[i]->k_in + 127) / 128);
     p.off_tickets[i] = p.ws;
     if (p.S[i] > 1) {
-      p.ws += align256(static_cast<size_t>(p.n_ob[i]) * 4);
+      p.ws += align256(static_cast<size_t>(p.n_ob[i]) * ncb * 4);
       p.off_part[i] = p.ws;
-      p.ws += align256(static_cast<size_t>(p.n_ob[i]) * p.S[i] * p.nb * 128 * sizeof(float));
+      p.ws += align256(static_cast<size_t>(p.n_ob[i]) * ncb * p.S[i] * part_cols * 128 *
+                       sizeof(float));
     } else {
       p.off_part[i] = p.ws;
     }
     p.off_xf[i] = p.ws;
-    p.ws += align256(static_cast<size_t>(p.nb) * W[i]->k_in * 4);
+    if (!p.gemv) p.ws += align256(static_cast<size_t>(p.nb) * W[i]->k_in * 4);
   }
   return p;
 }
@@ -192,14 +249,33 @@ int launch_gemv(int K, int cb, int kc, const TmkArgs& g, hipStream_t st) {
   }
 }
 
+// The x fold of every member (batch > 1), written once to the workspace.
+int launch_xfold(TmkArgs& g, int folds, hipStream_t st) {
+  const int items = g.total;
+  g.total = folds;
+  hipLaunchKernelGGL(xfold_kernel, dim3(static_cast<unsigned>((folds + 3) / 4)), dim3(256), 0, st, g);
+  g.total = items;
+  return hipGetLastError() == hipSuccess ? TRELLIS_OK : TRELLIS_ERR_LAUNCH;
+}
+
+// Batch >= 2: the x fold, the decode-once batched kernel, and (split-K) its reduction.
+int launch_bgemm(int K, int cb, int nc, TmkArgs& g, int folds, int nfold, hipStream_t st) {
+  int v = launch_xfold(g, folds, st);
+  if (v) return v;
+  switch (K) {
+    case 2: v = launch_bgemm_k<2>(cb, nc, g, st); break;
+    case 3: v = launch_bgemm_k<3>(cb, nc, g, st); break;
+    default: v = launch_bgemm_k<4>(cb, nc, g, st); break;
+  }
+  if (v || nfold == 0) return v;
+  return launch_bfold(cb, nc, nfold, g, st);
+}
+
 // The x fold of every member, then the decode-matmul.
 int launch_tmk(int K, int cb, int ks, TmkArgs& g, int folds, hipStream_t st) {
   if (g.batch > 1) {
-    const int items = g.total;
-    g.total = folds;
-    hipLaunchKernelGGL(xfold_kernel, dim3(static_cast<unsigned>((folds + 3) / 4)), dim3(256), 0, st, g);
-    g.total = items;
-    if (hipGetLastError() != hipSuccess) return TRELLIS_ERR_LAUNCH;
+    const int v = launch_xfold(g, folds, st);
+    if (v) return v;
   }
   switch (K) {
     case 2: return launch_tmk_k<2>(cb, ks, g, st);
@@ -354,11 +430,24 @@ int trellis_packed_linear_group(const trellis_desc* const* W, int count, const v
     m.n_ob = p.n_ob[i];
     m.S = p.S[i];
     m.item0 = item0;
-    item0 += p.n_ob[i] * p.S[i];
+    item0 += p.n_ob[i] * (p.gemv || p.tmk ? 1 : p.ncb) * p.S[i];
     m.tickets = reinterpret_cast<unsigned*>(ws + p.off_tickets[i]);
     m.part = reinterpret_cast<float*>(ws + p.off_part[i]);
     m.xf = reinterpret_cast<uint32_t*>(ws + p.off_xf[i]);
   }
+  // the members' item ranges must tile the grid exactly
+  if (item0 != p.total) return TRELLIS_ERR_LAUNCH;
+  // bfold_kernel workgroups: one per (block, column block) of every split-K member
+  int nfold = 0;
+  for (int i = 0; i < count; ++i) {
+    g.m[i].fold0 = nfold;
+    if (!p.gemv && !p.tmk && p.S[i] > 1) nfold += p.n_ob[i] * p.ncb;
+  }
+  if (env_int("TRELLIS_PLAN_LOG", 0))
+    std::fprintf(stderr, "trellis plan: batch=%d members=%d mode=%s kr=%d kc=%d nc=%d ncb=%d "
+                         "items=%d S0=%d ws=%zu\n",
+                 batch, count, p.gemv ? "gemv" : p.tmk ? "tmk" : "bgemm", p.kr, p.kc, p.nc,
+                 p.ncb, p.total, p.S[0], p.ws);
   const size_t xes = g.x_f16 ? 2 : 4, yes = g.y_f16 ? 2 : 4;
   for (int b0 = 0; b0 < batch; b0 += p.nb) {
     g.batch = batch - b0 < p.nb ? batch - b0 : p.nb;
@@ -369,8 +458,9 @@ int trellis_packed_linear_group(const trellis_desc* const* W, int count, const v
       g.m[i].chunk0 = chunk0;
       chunk0 += g.batch * ((W[i]->k_in + 127) / 128);
     }
-    v = p.gemv ? launch_gemv(W[0]->K, W[0]->codebook, p.kc, g, st)
-               : launch_tmk(W[0]->K, W[0]->codebook, p.ks, g, chunk0, st);
+    v = p.gemv  ? launch_gemv(W[0]->K, W[0]->codebook, p.kc, g, st)
+        : p.tmk ? launch_tmk(W[0]->K, W[0]->codebook, p.ks, g, chunk0, st)
+                : launch_bgemm(W[0]->K, W[0]->codebook, p.nc, g, chunk0, nfold, st);
     if (v) return v;
   }
   return TRELLIS_OK;
