@@ -45,7 +45,7 @@ typedef enum trellis_status {
   TRELLIS_ERR_SHAPE = 2,       /* n or k not a positive multiple of 16 */
   TRELLIS_ERR_BLOCK = 3,       /* Hadamard block not a power of 2 in [16,128] dividing the dim */
   TRELLIS_ERR_K = 4,           /* bits/weight outside {2,3,4} */
-  TRELLIS_ERR_V = 5,           /* vector dimension other than 1 */
+  TRELLIS_ERR_V = 5,           /* weights per trellis step other than 1 or 2 */
   TRELLIS_ERR_CODEBOOK = 6,    /* unknown codebook id */
   TRELLIS_ERR_NWORDS = 7,      /* nwords != 256*K/32 */
   TRELLIS_ERR_ALIGN = 8,       /* bits not 16-byte aligned, or a stride too small */
@@ -54,7 +54,7 @@ typedef enum trellis_status {
   TRELLIS_ERR_BATCH = 11,      /* batch < 1 */
   TRELLIS_ERR_RANGE = 12,      /* tile range outside the matrix */
   TRELLIS_ERR_LAUNCH = 13,     /* the HIP runtime rejected a launch */
-  TRELLIS_ERR_GROUP = 14       /* group of 0 or more than 8 linears, or mixed K / codebook */
+  TRELLIS_ERR_GROUP = 14       /* group of 0 or more than 8 linears, or mixed K / V / codebook */
 } trellis_status;
 
 /* One packed trellis linear as the loader record holds it (web/packed.js:53-62,
@@ -68,7 +68,11 @@ typedef struct trellis_desc {
   int32_t n_out;             /* rows, multiple of 16 */
   int32_t k_in;              /* cols, multiple of 16 */
   int32_t K;                 /* bits per weight: 2, 3 or 4 */
-  int32_t V;                 /* weights per trellis step: 1 */
+  int32_t V;                 /* weights per trellis step: 1 (the reference), or 2: the tile's
+                              * stream read as 128 steps of 2K bits, step u at stream bit
+                              * (127-u)*2K; the step's state gives weight 2u from the
+                              * codebook's first LCG iterate and weight 2u+1 from the second
+                              * (no reference counterpart: qtip.py:4 has V=1 only) */
   int32_t codebook;          /* enum trellis_codebook */
   int32_t block_in;          /* fit(k_in, 128) */
   int32_t block_out;         /* fit(n_out, 128) (web/packed.js:173-176) */
@@ -85,10 +89,10 @@ int trellis_workspace_bytes(const trellis_desc *W, int batch, size_t *bytes);
  * (web/packed.js:163-182) and its Python mirror linear() (scripts/run_packed_headless.py:87-99).
  *   x: [batch, k_in] with row stride ldx elements, dtype x_dtype (f16 or f32)
  *   y: [batch, n_out] with row stride ldy elements, dtype y_dtype (f16 or f32)
- * Every batch runs the decode-to-MFMA kernel: packed words are staged in LDS with
- * coalesced 16-byte loads, each lane decodes its part of a 16x16 tile straight into the
- * A operand of v_mfma_f32_16x16x32_f16, and batch rows are the B columns (up to 16 per
- * launch; larger batches run in chunks of 16 rows). */
+ * Batch 1 runs one decode-GEMV launch (gemv_kernel, x fold fused). Larger batches run the
+ * x fold once (xfold_kernel), then the decode-once batched kernel (bgemm_kernel: each
+ * weight tile decoded once per 128 batch columns and fed to exact fp16 MFMAs), and, when
+ * the launch plan splits k, the slice reduction and output fold (bfold_kernel). */
 int trellis_packed_linear(const trellis_desc *W, const void *x, int64_t ldx, int batch,
                           int x_dtype, void *y, int64_t ldy, int y_dtype, void *workspace,
                           size_t ws_bytes, void *stream);

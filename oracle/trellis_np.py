@@ -73,6 +73,37 @@ def codebook_values(states: np.ndarray, codebook: str) -> np.ndarray:
     return _fp16_pair_sum(lop3_raw(p))
 
 
+# V=2 (two weights per trellis step). The reference implements V=1 only (qtip.py:4 and
+# notes/qtip-exl3-spec.md:10, 21 name V=2 as QTIP's released setting, with a learned 2-D
+# LUT this repository does not ship). This build defines V=2 on the reference's computed
+# codebooks: the 16-bit state of step u yields weight 2u from the codebook's first LCG
+# iterate (exactly the V=1 value) and weight 2u+1 from the second iterate of the same
+# 32-bit map (MCG: s*C then s*C*C; 3INST/1MAD: x -> x*a + b applied twice), both through
+# the codebook's usual output stage (lop3 + fp16-halves sum, or byte sum).
+_LCG = {"mcg": (0xCBAC1FED, 0), "3inst": (89226354, 64248484), "1mad": (34038481, 76625530)}
+
+
+def lcg_next(p: np.ndarray, codebook: str) -> np.ndarray:
+    """One more iterate of the codebook's 32-bit affine map on a full 32-bit value."""
+    mul, add = _LCG[codebook]
+    x = np.asarray(p).astype(np.uint64) * np.uint64(mul) + np.uint64(add)
+    return (x & np.uint64(MASK32)).astype(np.uint32)
+
+
+def _output_stage(p: np.ndarray, codebook: str) -> np.ndarray:
+    if codebook == "1mad":
+        y = ((p & 255) + ((p >> 8) & 255) + ((p >> 16) & 255) + ((p >> 24) & 255))
+        return ((y.astype(np.float32) - np.float32(510.0))
+                / np.float32(147.800537109375)).astype(np.float32)
+    return _fp16_pair_sum(lop3_raw(p))
+
+
+def codebook_values_v2(states: np.ndarray, codebook: str):
+    """state (u16) -> (first, second) fp32 values of the V=2 codebook defined above."""
+    p1 = lcg_raw(states, codebook)
+    return _output_stage(p1, codebook), _output_stage(lcg_next(p1, codebook), codebook)
+
+
 def codebook_lut(codebook: str) -> np.ndarray:
     """All 2^16 states -> fp32 LUT (qtip.py:59-66)."""
     return codebook_values(np.arange(S, dtype=np.uint32), codebook)
@@ -160,9 +191,23 @@ def window_states(packed: np.ndarray, K: int, T: int = T_SEQ) -> np.ndarray:
     return (win & np.uint64(0xFFFF)).astype(np.uint32)
 
 
-def decode_packed_tiles(packed: np.ndarray, K: int, codebook: str = "mcg") -> np.ndarray:
-    """Packed words -> fp32 z-space tiles [ntiles, 256] (the bit-exact decode)."""
-    return codebook_values(window_states(packed, K), codebook)
+def decode_packed_tiles(packed: np.ndarray, K: int, codebook: str = "mcg",
+                        V: int = 1) -> np.ndarray:
+    """Packed words -> fp32 z-space tiles [ntiles, 256] (the bit-exact decode).
+
+    V=2: the stream is the same 256*K bits per tile, read as 128 steps of 2K bits (step u
+    at stream bits (127-u)*2K, i.e. window_states with symbol width 2K over T=128); the
+    state of step u gives weights 2u and 2u+1 (codebook_values_v2)."""
+    if V == 1:
+        return codebook_values(window_states(packed, K), codebook)
+    if V != 2:
+        raise ValueError("V must be 1 or 2")
+    st = window_states(packed, 2 * K, T=T_SEQ // 2)
+    v0, v1 = codebook_values_v2(st, codebook)
+    out = np.empty((st.shape[0], T_SEQ), np.float32)
+    out[:, 0::2] = v0
+    out[:, 1::2] = v1
+    return out
 
 
 # ----------------------------------------------------------------------------- tile layout
@@ -285,7 +330,7 @@ def w_hat_from_record(packed: np.ndarray, rec: IPRecord) -> np.ndarray:
     """restore(decode(bits)) from the packed words and stored f16/f32 metadata: the
     definition the packed-linear call must match (SURVEY: y = restore(decode(bits)) @ x;
     packed.js:51-52 folds scale into isc, which restore applies as zq*scale)."""
-    zt = decode_packed_tiles(packed, rec.K, rec.codebook)
+    zt = decode_packed_tiles(packed, rec.K, rec.codebook, rec.V)
     zq = tiles_to_matrix(zt, rec.n, rec.k)
     return restore(zq, rec.scale, rec.su.astype(np.float64), rec.sv.astype(np.float64),
                    rec.isc.astype(np.float64), rec.osc.astype(np.float64))
@@ -303,7 +348,7 @@ def packed_linear_fold(packed: np.ndarray, rec: IPRecord, x: np.ndarray) -> np.n
     """The reference's IP-folded evaluation order (web/packed.js:163-181):
     xf = Hb_k((isc*scale) * (su*x)); t = zq @ xf; y = sv * (osc * Hb_n(t)).
     float64 arithmetic, fp32 fold of scale into isc as the loader does (:51-52)."""
-    zt = decode_packed_tiles(packed, rec.K, rec.codebook)
+    zt = decode_packed_tiles(packed, rec.K, rec.codebook, rec.V)
     zq = tiles_to_matrix(zt, rec.n, rec.k).astype(np.float64)
     isc_s = (rec.isc.astype(np.float32) * rec.scale).astype(np.float64)
     x64 = np.atleast_2d(np.asarray(x, np.float64))
@@ -322,8 +367,15 @@ def rel_err(got: np.ndarray, ref: np.ndarray) -> float:
 
 
 # ----------------------------------------------------------------------------- synthetic records
+def codebook_rms_v2(codebook: str) -> float:
+    """RMS over both values of all 2^16 V=2 states, float64."""
+    v0, v1 = codebook_values_v2(np.arange(S, dtype=np.uint32), codebook)
+    both = np.concatenate([v0, v1]).astype(np.float64)
+    return float(np.sqrt(np.mean(both * both)))
+
+
 def synthetic_record(n: int, k: int, K: int, seed: int, codebook: str = "mcg",
-                     mean1_scales: bool = True):
+                     mean1_scales: bool = True, V: int = 1):
     """Seeded synthetic packed linear as BASELINE configs 2-5 describe: uniform random
     u32 bits (every stream is a valid tail-biting path), ±1 su/sv, per-matrix scale
     fp16(0.02 / RMS_codebook) stored as f32, isc/osc mean-1 (or ones)."""
@@ -345,6 +397,7 @@ def synthetic_record(n: int, k: int, K: int, seed: int, codebook: str = "mcg",
     else:
         isc = np.ones(k, np.float16)
         osc = np.ones(n, np.float16)
-    scale = np.float32(np.float16(0.02 / codebook_rms(codebook)))
-    rec = IPRecord(n, k, K, su, sv, isc, osc, scale, codebook=codebook)
+    rms = codebook_rms(codebook) if V == 1 else codebook_rms_v2(codebook)
+    scale = np.float32(np.float16(0.02 / rms))
+    rec = IPRecord(n, k, K, su, sv, isc, osc, scale, codebook=codebook, V=V)
     return bits, rec

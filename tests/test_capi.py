@@ -43,7 +43,7 @@ def _desc(te, **kw):
 
 @pytest.mark.parametrize("kw,status", [
     (dict(bits=None), 1), (dict(n_out=100), 2), (dict(k_in=0), 2), (dict(K=5, nwords=40), 4),
-    (dict(V=2), 5), (dict(codebook=3), 6), (dict(nwords=23), 7), (dict(block_in=64 + 32), 3),
+    (dict(V=3), 5), (dict(V=0), 5), (dict(codebook=3), 6), (dict(nwords=23), 7), (dict(block_in=64 + 32), 3),
     (dict(block_out=256), 3), (dict(bits=8), 8),
 ])
 def test_validation_codes(te, kw, status):

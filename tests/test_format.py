@@ -62,3 +62,24 @@ def test_sharded_manifest(te, tmp_path):
     assert not os.path.exists(tmp_path / "weights.bin")
     got, _, _ = te.read_packed(str(tmp_path))
     assert np.array_equal(got["model.layers.3.self_attn.q_proj.weight"].bits, r.bits)
+
+
+def test_v2_roundtrip_and_default(te, tmp_path):
+    """The V extension key is written only for V != 1 and read back; absent means V=1."""
+    bits, r = tn.synthetic_record(32, 64, 3, 5, V=2)
+    rec2 = te.PackedRecord(32, 64, 3, bits, r.su, r.sv, r.isc, r.osc, float(r.scale), V=2)
+    rec1 = _rec(te, 32, 64, 3, 6)
+    te.write_packed(str(tmp_path), {"a": rec2, "b": rec1})
+    man = json.load(open(tmp_path / "manifest.json"))
+    assert man["a"]["V"] == 2 and "V" not in man["b"]
+    got, _, _ = te.read_packed(str(tmp_path))
+    assert got["a"].V == 2 and got["b"].V == 1
+    assert np.array_equal(got["a"].bits, bits)
+
+
+def test_validate_rejects_bad_v(te):
+    import pytest
+    bits, r = tn.synthetic_record(32, 64, 3, 5)
+    rec = te.PackedRecord(32, 64, 3, bits, r.su, r.sv, r.isc, r.osc, float(r.scale), V=3)
+    with pytest.raises(ValueError):
+        rec.validate()

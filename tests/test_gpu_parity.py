@@ -27,7 +27,7 @@ def _say(msg):
 
 def make_linear(te, bits, rec, device):
     r = te.PackedRecord(rec.n, rec.k, rec.K, bits, rec.su, rec.sv, rec.isc, rec.osc,
-                        float(rec.scale), codebook=rec.codebook)
+                        float(rec.scale), codebook=rec.codebook, V=rec.V)
     return te.PackedLinear(r, device=device)
 
 
@@ -255,3 +255,33 @@ def test_group_many_column_blocks(te, gpu_device):
     for (bits, rec, _), x, y in zip(members, xs, ys):
         want = tn.packed_linear_ref(bits, rec, x.cpu().numpy())
         assert tn.rel_err(y.cpu().numpy(), want) < TOL
+
+
+# ------------------------------------------------------------------ V=2 (this build's definition)
+@pytest.mark.parametrize("K", [2, 3, 4])
+@pytest.mark.parametrize("cb", ["mcg", "3inst", "1mad"])
+def test_v2_decode_tiles_bit_exact(te, gpu_device, K, cb):
+    """V=2 decoded tiles bit-exact against the oracle over a 512x2048 random record
+    (4096 tiles, 524k states), and a sub-range call."""
+    _say(f"[v2 decode] K={K} cb={cb}")
+    bits, rec = tn.synthetic_record(512, 2048, K, seed=K * 11 + tn.CODEBOOK_IDS[cb], codebook=cb,
+                                    V=2)
+    lin = make_linear(te, bits, rec, gpu_device)
+    got = lin.decode_tiles().cpu().numpy()
+    want = tn.decode_packed_tiles(bits, K, cb, V=2)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    sub = lin.decode_tiles(333, 41).cpu().numpy()
+    assert np.array_equal(sub.view(np.uint32), want[333:374].view(np.uint32))
+
+
+@pytest.mark.parametrize("n,k,K,cb", [(256, 512, 3, "mcg"), (1536, 576, 2, "3inst"),
+                                      (384, 2048, 4, "1mad"), (2048, 4096, 3, "mcg")])
+@pytest.mark.parametrize("batch", [1, 5, 64])
+def test_v2_linear_vs_oracle(te, gpu_device, n, k, K, cb, batch):
+    _say(f"[v2 linear] n={n} k={k} K={K} cb={cb} batch={batch}")
+    bits, rec = tn.synthetic_record(n, k, K, seed=n + k + K, codebook=cb, V=2)
+    W = tn.w_hat_from_record(bits, rec)
+    lin = make_linear(te, bits, rec, gpu_device)
+    x = np.random.default_rng(batch).standard_normal((batch, k)).astype(np.float16)
+    y = lin(torch.from_numpy(x).to(gpu_device)).cpu().numpy()
+    assert tn.rel_err(y, x.astype(np.float64) @ W.T) < TOL

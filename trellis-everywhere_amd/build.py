@@ -13,8 +13,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libtrellis_amd.so")
-SOURCES = ["trellis_amd.hip", "tmk_k2.hip", "tmk_k3.hip", "tmk_k4.hip"]
-HEADERS = ["decode.h", "tmk.h", "gemv.h", "bgemm.h", "tmk_launch.h"]
+SOURCES = ["trellis_amd.hip", "kernels_k2.hip", "kernels_k3.hip", "kernels_k4.hip"]
+HEADERS = ["decode.h", "common.h", "gemv.h", "bgemm.h", "launch.h"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"

@@ -9,7 +9,7 @@
 //     then stored to the other half of a double-buffered LDS area; one barrier per step;
 //   * each wave decodes a tile of each of its bands once, straight into the A operand of
 //     v_mfma_f32_16x16x32_f16 (the exact (hi, lo) pair against the duplicated activation,
-//     as in tmk_kernel), and issues NC MFMAs per band against the NC batch chunks, so the
+//     common.h), and issues NC MFMAs per band against the NC batch chunks, so the
 //     decode is amortised over all NB columns and each B fragment read from LDS serves
 //     both bands;
 //   * the B rows are padded by 4 words so the 16 batch rows of a fragment fall in
@@ -21,14 +21,14 @@
 //     ~2 us each, with one workgroup's worth of loads in flight.
 #pragma once
 
-#include "tmk.h"
+#include "common.h"
 
 namespace trellis {
 
 // y[b0 + b] = sv * osc * Hb_n(t[b]) for the nbv batch columns staged in LDS as
 // t[b][128]; one column per wave at a time (256-thread workgroups).
 template <int CB>
-__device__ __forceinline__ void bg_out_fold(const TmkArgs& g, const TmkMat& m, const float* tl,
+__device__ __forceinline__ void bg_out_fold(const LinArgs& g, const LinMat& m, const float* tl,
                                             int ob, int b0, int nbv, int rows) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const float nrm = 1.0f / sqrtf(static_cast<float>(m.block_out));
@@ -64,8 +64,8 @@ __device__ __forceinline__ void bg_out_fold(const TmkArgs& g, const TmkMat& m, c
 // k-step: 8 tile columns for up to 64 batch columns, 4 for 128 (LDS holds two B steps)
 template <int NC> struct BgStep { static constexpr int KT = NC <= 4 ? 8 : 4; };
 
-template <int K, int CB, int NC>
-__global__ __launch_bounds__(256) void bgemm_kernel(TmkArgs g) {
+template <int K, int CB, int V, int NC>
+__global__ __launch_bounds__(256) void bgemm_kernel(LinArgs g) {
   constexpr int NWK = 8 * K;
   constexpr int BG_KT = BgStep<NC>::KT;            // tile columns per k-step
   constexpr int BG_XW = BG_KT * 16 + 4;            // LDS words per B row (+4: bank spread)
@@ -83,7 +83,7 @@ __global__ __launch_bounds__(256) void bgemm_kernel(TmkArgs g) {
 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int mi = locate_mat(g, blockIdx.x, false);
-  const TmkMat& m = g.m[mi];
+  const LinMat& m = g.m[mi];
   const int local = blockIdx.x - m.item0;
   const int ncb = (g.batch + NB - 1) / NB;
   const int sl = local % m.S, obcb = local / m.S;
@@ -137,7 +137,7 @@ __global__ __launch_bounds__(256) void bgemm_kernel(TmkArgs g) {
   };
 
   const int r = lane & 15, gq = lane >> 4;
-  const QuadPos qp = quad_pos<K>(r, gq);
+  const QuadPos qp = quad_pos_v<K, V>(r, gq);
   float4_t acc[2][NC];
 #pragma unroll
   for (int b = 0; b < 2; ++b)
@@ -155,8 +155,8 @@ __global__ __launch_bounds__(256) void bgemm_kernel(TmkArgs g) {
     for (int t = 0; t < BG_KT; ++t) {
       const uint32_t* t0 = &bst[buf][wave][t * NWK];
       const uint32_t* t1 = &bst[buf][wave][(BG_KT + t) * NWK];
-      const half8_t A0 = decode_a<K, CB>(t0[qp.wa], t0[qp.wb], qp.sh);
-      const half8_t A1 = decode_a<K, CB>(t1[qp.wa], t1[qp.wb], qp.sh);
+      const half8_t A0 = decode_a<K, CB, V>(t0[qp.wa], t0[qp.wb], qp.sh);
+      const half8_t A1 = decode_a<K, CB, V>(t1[qp.wa], t1[qp.wb], qp.sh);
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         const half8_t B = __builtin_bit_cast(
@@ -192,11 +192,11 @@ __global__ __launch_bounds__(256) void bgemm_kernel(TmkArgs g) {
 // block) adds the S partial blocks in slice order (deterministic), then folds. Runs after
 // bgemm_kernel, so plain loads see its plain stores.
 template <int CB, int NC>
-__global__ __launch_bounds__(256) void bfold_kernel(TmkArgs g) {
+__global__ __launch_bounds__(256) void bfold_kernel(LinArgs g) {
   constexpr int NB = 16 * NC;
   __shared__ __align__(16) float tl[NB * 128];
   const int mi = locate_fold(g, blockIdx.x);
-  const TmkMat& m = g.m[mi];
+  const LinMat& m = g.m[mi];
   const int ncb = (g.batch + NB - 1) / NB;
   const int local = blockIdx.x - m.fold0;
   const int ob = local / ncb, cb = local % ncb;

@@ -1,0 +1,156 @@
+// common.h — what the gfx950 trellis kernels share: launch arguments of a group of packed
+// linears, activation access, the lane-shuffle block Hadamard, the batched x fold, and the
+// decode of one tile straight into the A operand of v_mfma_f32_16x16x32_f16.
+//
+// The incoherence-processing fold (web/packed.js:163-182 runs it as seven dispatches per
+// linear) is split around the decode-matmul: xf = Hb_k(isc_scaled * su * x) on the input
+// side (fused in gemv_kernel at batch 1, xfold_kernel once per call for batch > 1) and
+// y = sv * osc * Hb_n(t) on the output side (in the kernels' epilogues).
+//
+// Decode to MFMA: lane l = (tile row r = l%16, column group g = l/16) decodes the 4
+// weights of columns 4g..4g+3 (decode.h). The codebook's lop3 result is the fp16 pair
+// (hi, lo) of a weight; its two halves are two adjacent k elements of the A operand and
+// the B operand holds the activation twice at those positions, so the MFMA accumulates
+// (hi + lo) * x in fp32 and the exact codebook value (the fp32 sum of the halves,
+// qtip.py:28-29) is never rounded.
+#pragma once
+
+#include "decode.h"
+
+namespace trellis {
+
+constexpr int MAX_GROUP = 8;   // linears per launch
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+struct LinMat {
+  const uint32_t* bits;
+  const float* su;
+  const float* sv;
+  const float* isc;     // isc_scaled = f32(isc) * scale
+  const float* osc;
+  const void* x;
+  void* y;
+  uint32_t* xf;         // workspace: [batch][k] fp16 (x,x) pairs
+  float* part;          // workspace: split-K partial sums (S > 1)
+  unsigned* tickets;    // workspace: [n_ob] arrival counters (batch 1, S > 1), zero between calls
+  long long ldx, ldy;
+  int n, k, tiles_in, block_in, block_out;
+  int n_ob, S;
+  int item0;            // first group-wide work item of this matrix
+  int chunk0;           // first group-wide x-fold job of this matrix
+  int fold0;            // first group-wide bfold_kernel workgroup of this matrix
+};
+
+struct LinArgs {
+  LinMat m[MAX_GROUP];
+  int nmat;
+  int total;            // work items of the launched kernel
+  int nwords;
+  int batch;            // batch rows of the call
+  int x_f16, y_f16;
+  int kr;               // tile columns per k-range
+};
+
+// Activation i of an f16 or f32 array, read as the aligned u32 word holding it so the
+// load is branch-free (f16 arrays must be 4-byte aligned with an even row stride).
+__device__ __forceinline__ uint32_t load_act_word(const void* p, long long i, int is_f16) {
+  const long long byte = is_f16 ? ((2 * i) & ~3LL) : 4 * i;
+  return *reinterpret_cast<const uint32_t*>(static_cast<const char*>(p) + byte);
+}
+
+__device__ __forceinline__ float act_value(uint32_t w, long long i, int is_f16) {
+  if (!is_f16) return __builtin_bit_cast(float, w);
+  const uint16_t h = static_cast<uint16_t>((i & 1) ? (w >> 16) : (w & 0xFFFFu));
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+// Butterflies of a normalized-free block Hadamard (block B <= 128) on a 128-element
+// chunk held as lo = e[lane], hi = e[lane + 64].
+__device__ __forceinline__ void fwht_chunk(float& lo, float& hi, int B, int lane) {
+  for (int h = 1; h < B && h < 64; h <<= 1) {
+    const float plo = __shfl_xor(lo, h);
+    const float phi = __shfl_xor(hi, h);
+    const bool upper = (lane & h) != 0;
+    lo = upper ? plo - lo : lo + plo;
+    hi = upper ? phi - hi : hi + phi;
+  }
+  if (B == 128) {
+    const float a = lo, b = hi;
+    lo = a + b;
+    hi = a - b;
+  }
+}
+
+__device__ __forceinline__ uint32_t dup_half(float v) {
+  const _Float16 h = static_cast<_Float16>(v);
+  const uint16_t u = __builtin_bit_cast(uint16_t, h);
+  return (static_cast<uint32_t>(u) << 16) | u;
+}
+
+__device__ __forceinline__ int locate_fold(const LinArgs& g, int it) {
+  int mi = 0;
+#pragma unroll
+  for (int j = 1; j < MAX_GROUP; ++j)
+    if (j < g.nmat && it >= g.m[j].fold0) mi = j;
+  return mi;
+}
+
+__device__ __forceinline__ int locate_mat(const LinArgs& g, int it, bool by_chunk) {
+  int mi = 0;
+#pragma unroll
+  for (int j = 1; j < MAX_GROUP; ++j)
+    if (j < g.nmat && it >= (by_chunk ? g.m[j].chunk0 : g.m[j].item0)) mi = j;
+  return mi;
+}
+
+// ---------------------------------------------------------------- x fold
+// One wave per (matrix, batch row, 128-column chunk): xf = Hb_k(isc * su * x) scaled by
+// 1/sqrt(block_in), stored as (x,x) fp16 pairs. Defined in one translation unit only.
+#ifdef TRELLIS_XFOLD_DEFINE
+__global__ __launch_bounds__(256) void xfold_kernel(LinArgs g) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int job = blockIdx.x * 4 + wave;
+  if (job >= g.total) return;
+  const int mi = locate_mat(g, job, true);
+  const LinMat& m = g.m[mi];
+  const int local = job - m.chunk0;
+  const int nch = (m.k + 127) / 128;
+  const int b = local / nch, ch = local % nch;
+  const int kvalid = min(128, m.k - ch * 128);
+  const int e0 = lane, e1 = lane + 64;
+  const int c0i = ch * 128 + min(e0, kvalid - 1), c1i = ch * 128 + min(e1, kvalid - 1);
+  const long long x0i = b * m.ldx + c0i, x1i = b * m.ldx + c1i;
+  const uint32_t w0 = load_act_word(m.x, x0i, g.x_f16);
+  const uint32_t w1 = load_act_word(m.x, x1i, g.x_f16);
+  const float s0 = m.su[c0i] * m.isc[c0i], s1 = m.su[c1i] * m.isc[c1i];
+  float lo = e0 < kvalid ? act_value(w0, x0i, g.x_f16) * s0 : 0.0f;
+  float hi = e1 < kvalid ? act_value(w1, x1i, g.x_f16) * s1 : 0.0f;
+  fwht_chunk(lo, hi, m.block_in, lane);
+  const float nrm = 1.0f / sqrtf(static_cast<float>(m.block_in));
+  uint32_t* dst = m.xf + static_cast<size_t>(b) * m.k + ch * 128;
+  if (e0 < kvalid) dst[e0] = dup_half(lo * nrm);
+  if (e1 < kvalid) dst[e1] = dup_half(hi * nrm);
+}
+#endif
+
+// ---------------------------------------------------------------- decode -> MFMA
+// The A operand of one band-tile for this lane (decode_quad). 1MAD yields (y - 510) as an
+// exact fp16 in the low half (the division by 147.800537109375 follows the sum).
+template <int K, int CB, int V = 1>
+__device__ __forceinline__ half8_t decode_a(uint32_t wlo, uint32_t whi, int sh) {
+  uint32_t a4[4];
+  decode_quad<K, CB, V>(wlo, whi, sh, a4);
+  if constexpr (CB == CB_1MAD) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const _Float16 h = static_cast<_Float16>(static_cast<float>(static_cast<int>(a4[q]) - 510));
+      a4[q] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h));
+    }
+  }
+  return __builtin_bit_cast(half8_t, a4);
+}
+
+}  // namespace trellis

@@ -87,12 +87,51 @@ __device__ __forceinline__ QuadPos quad_pos(int r, int g) {
   return {o3 >> 5, ((o3 >> 5) + 1) % NW, o3 & 31};
 }
 
-// Raw codebook outputs (cb_raw) of the lane's four windows.
-template <int K, int CB>
+// V=2 (two weights per trellis step; the reference has V=1 only, this build's definition):
+// the tile's stream is read as 128 steps of 2K bits, step u at stream bit (127-u)*2K; the
+// state of step u gives weight 2u from the codebook's first LCG iterate and weight 2u+1 from
+// the second iterate of the same 32-bit map. Lane (r, g) holds columns 4g..4g+3, i.e. steps
+// u0 = 8r + 2g and u1 = u0 + 1; u1's window starts at o1 = (126 - 8r - 2g) * 2K and u0's
+// sits 2K bits above it in the same funnel (16 + 2K <= 24 bits).
+template <int K>
+__device__ __forceinline__ QuadPos quad_pos_v2(int r, int g) {
+  constexpr int NW = 8 * K;
+  const int o1 = (126 - 8 * r - 2 * g) * 2 * K;
+  return {o1 >> 5, ((o1 >> 5) + 1) % NW, o1 & 31};
+}
+
+template <int K, int V>
+__device__ __forceinline__ QuadPos quad_pos_v(int r, int g) {
+  if constexpr (V == 2)
+    return quad_pos_v2<K>(r, g);
+  else
+    return quad_pos<K>(r, g);
+}
+
+// Output stage of a full 32-bit LCG value: lop3 pair, or 1MAD's byte sum.
+template <int CB>
+__device__ __forceinline__ uint32_t cb_out(uint32_t p) {
+  if constexpr (CB == CB_1MAD)
+    return byte_sum(p);
+  else
+    return lop3_pair(p);
+}
+
+// Raw codebook outputs (cb_raw) of the lane's four weights (columns 4g..4g+3).
+template <int K, int CB, int V = 1>
 __device__ __forceinline__ void decode_quad(uint32_t wlo, uint32_t whi, int sh, uint32_t (&raw)[4]) {
   const uint32_t u = __builtin_amdgcn_alignbit(whi, wlo, sh);
+  if constexpr (V == 2) {
 #pragma unroll
-  for (int q = 0; q < 4; ++q) raw[q] = cb_raw<CB>((u >> (K * (3 - q))) & 0xFFFFu);
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t p = lcg_p<CB>((u >> (2 * K * (1 - h))) & 0xFFFFu);
+      raw[2 * h] = cb_out<CB>(p);
+      raw[2 * h + 1] = cb_out<CB>(p * Lcg<CB>::MUL + Lcg<CB>::ADD);
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) raw[q] = cb_raw<CB>((u >> (K * (3 - q))) & 0xFFFFu);
+  }
 }
 
 }  // namespace trellis

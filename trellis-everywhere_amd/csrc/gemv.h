@@ -1,9 +1,9 @@
 // gemv.h — batch-1 packed linear for gfx950: a pipelined decode-GEMV.
 //
-// Same arithmetic as tmk_kernel (decode straight into the A operand of
-// v_mfma_f32_16x16x32_f16, the codebook's fp16 pair (hi, lo) against a duplicated
-// activation, fp32 accumulation), organised for batch 1, where the decode's VALU work and
-// fixed per-launch latencies, not HBM, set the time:
+// The decode goes straight into the A operand of v_mfma_f32_16x16x32_f16 (the codebook's
+// fp16 pair (hi, lo) against a duplicated activation, fp32 accumulation: common.h),
+// organised for batch 1, where the decode's VALU work and fixed per-launch latencies, not
+// HBM, set the time:
 //
 //   * Work item = one matrix x one 128-row output block (8 bands of 16 rows) x one
 //     k-range of `kr` tile columns, run by one 16-wave workgroup (one per CU): waves w and
@@ -23,7 +23,7 @@
 //     (deterministic) before the fold. sv * osc is loaded at kernel start.
 #pragma once
 
-#include "tmk.h"
+#include "common.h"
 
 namespace trellis {
 
@@ -32,8 +32,8 @@ constexpr int GEMV_MAX_KR = 256;  // tile columns per k-range (4096 activations)
 constexpr int GEMV_PF = 2;        // pipeline stages in flight per wave
 constexpr int GEMV_G = 4;         // tiles decoded before their MFMAs are issued
 
-template <int K, int CB, int KC, int PF>
-__global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(TmkArgs g) {
+template <int K, int CB, int V, int KC, int PF>
+__global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
   constexpr int NWK = 8 * K;                 // words per tile
   constexpr int SW = KC * NWK;               // words per wave-stage
   constexpr int CH = SW / 4;                 // 16-byte chunks per wave-stage
@@ -46,7 +46,7 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(TmkArgs g) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int bl = wave & 7, half = wave >> 3;     // band of the block, half of the k-range
   const int mi = locate_mat(g, blockIdx.x, false);
-  const TmkMat& m = g.m[mi];
+  const LinMat& m = g.m[mi];
   const int local = blockIdx.x - m.item0;
   const int ob = local / m.S, sl = local % m.S;
   const int c0 = sl * g.kr;                          // first tile column of the k-range
@@ -123,7 +123,7 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(TmkArgs g) {
   // ---- main loop: stage s is moved from registers to the wave's LDS buffer, the load
   // of stage s + PF is issued into the freed registers, then stage s is decoded
   const int r = lane & 15, gq = lane >> 4;
-  const QuadPos qp = quad_pos<K>(r, gq);
+  const QuadPos qp = quad_pos_v<K, V>(r, gq);
   float4_t acc = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
   half8_t Bv[GEMV_G];
   auto stage = [&](int s, u32x4_t (&src)[LOADS]) {
@@ -150,7 +150,7 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(TmkArgs g) {
       for (int j = 0; j < GEMV_G; ++j)
         Bv[j] = __builtin_bit_cast(half8_t, *reinterpret_cast<const u32x4_t*>(xst + (j0 + j) * 16));
 #pragma unroll
-      for (int j = 0; j < GEMV_G; ++j) A[j] = decode_a<K, CB>(wlo[j], whi[j], qp.sh);
+      for (int j = 0; j < GEMV_G; ++j) A[j] = decode_a<K, CB, V>(wlo[j], whi[j], qp.sh);
 #pragma unroll
       for (int j = 0; j < GEMV_G; ++j) {
         if (j & 1)
@@ -167,7 +167,7 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(TmkArgs g) {
       for (int j = 0; j < jn; ++j) {
         const half8_t B = __builtin_bit_cast(half8_t, *reinterpret_cast<const u32x4_t*>(xst + j * 16));
         const uint32_t* tp = mystg + j * NWK;
-        const half8_t A = decode_a<K, CB>(tp[qp.wa], tp[qp.wb], qp.sh);
+        const half8_t A = decode_a<K, CB, V>(tp[qp.wa], tp[qp.wb], qp.sh);
         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, acc, 0, 0, 0);
       }
     }

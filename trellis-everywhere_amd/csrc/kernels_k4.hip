@@ -1,0 +1,8 @@
+// Decode-matmul kernel instantiations for K=4 bits per weight.
+#define TRELLIS_KERNELS_INSTANTIATE
+#include "launch.h"
+
+namespace trellis {
+template int launch_gemv_k<4>(int, int, int, const LinArgs&, hipStream_t);
+template int launch_bgemm_k<4>(int, int, int, const LinArgs&, hipStream_t);
+}  // namespace trellis

@@ -1,0 +1,99 @@
+// launch.h — host launchers of the decode-matmul kernels, one translation unit per K
+// (kernels_k2.hip, kernels_k3.hip, kernels_k4.hip) so the instantiations build in parallel.
+// Every launcher returns 0 or TRELLIS_ERR_LAUNCH.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "bgemm.h"
+#include "common.h"
+#include "gemv.h"
+
+namespace trellis {
+
+// gemv_kernel<K, cb, V, kc> over g.total items (batch 1, k-ranges of g.kr tiles).
+template <int K>
+int launch_gemv_k(int cb, int V, int kc, const LinArgs& g, hipStream_t st);
+
+// bgemm_kernel<K, cb, V, nc> over g.total items (the x fold has been launched before it).
+template <int K>
+int launch_bgemm_k(int cb, int V, int nc, const LinArgs& g, hipStream_t st);
+
+// bfold_kernel<cb, nc> over nfold workgroups (after a split-K bgemm_kernel).
+int launch_bfold(int cb, int nc, int nfold, const LinArgs& g, hipStream_t st);
+
+#ifdef TRELLIS_BFOLD_DEFINE
+template <int CB>
+static int launch_bfold_cb(int nc, int nfold, const LinArgs& g, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>(nfold));
+  switch (nc) {
+    case 1: hipLaunchKernelGGL((bfold_kernel<CB, 1>), grid, dim3(256), 0, st, g); break;
+    case 2: hipLaunchKernelGGL((bfold_kernel<CB, 2>), grid, dim3(256), 0, st, g); break;
+    case 4: hipLaunchKernelGGL((bfold_kernel<CB, 4>), grid, dim3(256), 0, st, g); break;
+    default: hipLaunchKernelGGL((bfold_kernel<CB, 8>), grid, dim3(256), 0, st, g); break;
+  }
+  return hipGetLastError() == hipSuccess ? 0 : 13;
+}
+
+int launch_bfold(int cb, int nc, int nfold, const LinArgs& g, hipStream_t st) {
+  switch (cb) {
+    case CB_MCG: return launch_bfold_cb<CB_MCG>(nc, nfold, g, st);
+    case CB_3INST: return launch_bfold_cb<CB_3INST>(nc, nfold, g, st);
+    default: return launch_bfold_cb<CB_1MAD>(nc, nfold, g, st);
+  }
+}
+#endif
+
+#ifdef TRELLIS_KERNELS_INSTANTIATE
+template <int K, int CB, int V>
+static int launch_gemv_kc(int kc, const LinArgs& g, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>(g.total));
+  if (kc == 8)
+    hipLaunchKernelGGL((gemv_kernel<K, CB, V, 8, GEMV_PF>), grid, dim3(64 * GEMV_WAVES), 0, st, g);
+  else
+    hipLaunchKernelGGL((gemv_kernel<K, CB, V, 16, GEMV_PF>), grid, dim3(64 * GEMV_WAVES), 0, st, g);
+  return hipGetLastError() == hipSuccess ? 0 : 13;
+}
+
+template <int K, int CB>
+static int launch_gemv_v(int V, int kc, const LinArgs& g, hipStream_t st) {
+  return V == 2 ? launch_gemv_kc<K, CB, 2>(kc, g, st) : launch_gemv_kc<K, CB, 1>(kc, g, st);
+}
+
+template <int K>
+int launch_gemv_k(int cb, int V, int kc, const LinArgs& g, hipStream_t st) {
+  switch (cb) {
+    case CB_MCG: return launch_gemv_v<K, CB_MCG>(V, kc, g, st);
+    case CB_3INST: return launch_gemv_v<K, CB_3INST>(V, kc, g, st);
+    default: return launch_gemv_v<K, CB_1MAD>(V, kc, g, st);
+  }
+}
+
+template <int K, int CB, int V>
+static int launch_bgemm_nc(int nc, const LinArgs& g, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>(g.total));
+  switch (nc) {
+    case 1: hipLaunchKernelGGL((bgemm_kernel<K, CB, V, 1>), grid, dim3(256), 0, st, g); break;
+    case 2: hipLaunchKernelGGL((bgemm_kernel<K, CB, V, 2>), grid, dim3(256), 0, st, g); break;
+    case 4: hipLaunchKernelGGL((bgemm_kernel<K, CB, V, 4>), grid, dim3(256), 0, st, g); break;
+    default: hipLaunchKernelGGL((bgemm_kernel<K, CB, V, 8>), grid, dim3(256), 0, st, g); break;
+  }
+  return hipGetLastError() == hipSuccess ? 0 : 13;
+}
+
+template <int K, int CB>
+static int launch_bgemm_v(int V, int nc, const LinArgs& g, hipStream_t st) {
+  return V == 2 ? launch_bgemm_nc<K, CB, 2>(nc, g, st) : launch_bgemm_nc<K, CB, 1>(nc, g, st);
+}
+
+template <int K>
+int launch_bgemm_k(int cb, int V, int nc, const LinArgs& g, hipStream_t st) {
+  switch (cb) {
+    case CB_MCG: return launch_bgemm_v<K, CB_MCG>(V, nc, g, st);
+    case CB_3INST: return launch_bgemm_v<K, CB_3INST>(V, nc, g, st);
+    default: return launch_bgemm_v<K, CB_1MAD>(V, nc, g, st);
+  }
+}
+#endif
+
+}  // namespace trellis

@@ -1,5 +1,6 @@
-// trellis_amd.hip — C ABI (include/trellis_amd.h) and launchers of the gfx950 trellis
-// kernels: the bit-exact tile decode and the fused decode-GEMV.
+// trellis_amd.hip — C ABI (include/trellis_amd.h): validation, launch planning, the
+// bit-exact tile decode kernel and the dispatch to the decode-matmul kernels (gemv_kernel at
+// batch 1, xfold_kernel + bgemm_kernel (+ bfold_kernel) above).
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
@@ -10,7 +11,7 @@
 #include "decode.h"
 #define TRELLIS_XFOLD_DEFINE
 #define TRELLIS_BFOLD_DEFINE
-#include "tmk_launch.h"
+#include "launch.h"
 
 using namespace trellis;
 
@@ -20,7 +21,7 @@ namespace {
 // One wave per tile, lane l = (tile row r = l%16, column group g = l/16): the same
 // decode_quad the matmul kernels run, each value stored as its exact fp32 (the fp16
 // halves summed in fp32; 1MAD divided as the reference does).
-template <int K, int CB>
+template <int K, int CB, int V>
 __global__ __launch_bounds__(256) void decode_tiles_kernel(const uint32_t* __restrict__ bits,
                                                            uint32_t tile0, uint32_t ntiles,
                                                            float* __restrict__ out) {
@@ -28,9 +29,9 @@ __global__ __launch_bounds__(256) void decode_tiles_kernel(const uint32_t* __res
   if (lt >= ntiles) return;
   const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
   const uint32_t* tp = bits + static_cast<size_t>(tile0 + lt) * (8 * K);
-  const QuadPos qp = quad_pos<K>(r, g);
+  const QuadPos qp = quad_pos_v<K, V>(r, g);
   uint32_t raw[4];
-  decode_quad<K, CB>(tp[qp.wa], tp[qp.wb], qp.sh, raw);
+  decode_quad<K, CB, V>(tp[qp.wa], tp[qp.wb], qp.sh, raw);
   float v[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q) v[q] = cb_exact<CB>(raw[q]);
@@ -51,7 +52,7 @@ int validate(const trellis_desc* W) {
   if (!W || !W->bits) return TRELLIS_ERR_NULL;
   if (W->n_out <= 0 || W->k_in <= 0 || W->n_out % 16 || W->k_in % 16) return TRELLIS_ERR_SHAPE;
   if (W->K < 2 || W->K > 4) return TRELLIS_ERR_K;
-  if (W->V != 1) return TRELLIS_ERR_V;
+  if (W->V != 1 && W->V != 2) return TRELLIS_ERR_V;
   if (W->codebook < 0 || W->codebook > 2) return TRELLIS_ERR_CODEBOOK;
   if (W->nwords != 256 * W->K / 32) return TRELLIS_ERR_NWORDS;
   if (!is_pow2(W->block_in) || W->block_in < 16 || W->block_in > 128 || W->k_in % W->block_in)
@@ -78,16 +79,14 @@ size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
 struct GroupPlan {
   int nb;              // batch rows per launch
-  int gemv;            // batch-1 gemv_kernel
-  int tmk;             // tmk_kernel in chunks of 16 rows (TRELLIS_TMK=1)
+  int gemv;            // batch-1 gemv_kernel (else bgemm_kernel)
   int nc, ncb;         // bgemm: 16-column chunks per workgroup, column blocks
   int kr;              // gemv / bgemm: tile columns per k-range
   int kc;              // gemv: tile columns per pipeline stage (8 or 16)
-  int ks;              // tmk: tile columns per work item (4, 8, 16, 32)
   int total;           // work items over the group
   int folds;           // x-fold jobs over the group
-  int n_ob[TMK_MAX_GROUP], S[TMK_MAX_GROUP];
-  size_t off_tickets[TMK_MAX_GROUP], off_part[TMK_MAX_GROUP], off_xf[TMK_MAX_GROUP];
+  int n_ob[MAX_GROUP], S[MAX_GROUP];
+  size_t off_tickets[MAX_GROUP], off_part[MAX_GROUP], off_xf[MAX_GROUP];
   size_t ws;           // workspace bytes
 };
 
@@ -135,9 +134,6 @@ int gemv_kr(const trellis_desc* const* W, int count) {
   return best;
 }
 
-// Batch > 1 (tmk_kernel): a work item is one 128-row output block x one k-slice of ks tile
-// columns: the largest ks in {32, 16} that still gives >= 256 items (one per CU), else 8
-// (TRELLIS_TMK_TARGET overrides the 256; TRELLIS_TMK_KS forces 4, 8, 16 or 32).
 // Batch >= 2 (bgemm_kernel): NC 16-column batch chunks per workgroup (up to 128 columns),
 // a work item is one 128-row block x one column block x one k-range of kr tile columns
 // (a multiple of the k-step, 8 tiles up to 64 columns, else 4). A workgroup has one wave
@@ -187,49 +183,30 @@ int bgemm_kr(const trellis_desc* const* W, int count, int batch, int nc) {
 
 GroupPlan group_plan(const trellis_desc* const* W, int count, int batch) {
   GroupPlan p;
-  p.gemv = batch == 1 && env_int("TRELLIS_GEMV", 1) != 0;
-  p.tmk = !p.gemv && env_int("TRELLIS_TMK", 0) != 0;
-  p.nb = p.tmk ? (batch < TMK_MAX_BATCH ? batch : TMK_MAX_BATCH) : batch;
+  p.gemv = batch == 1;
+  p.nb = batch;
   p.nc = bgemm_nc(batch);
-  p.ncb = (batch + 16 * p.nc - 1) / (16 * p.nc);
-  p.kr = p.gemv ? gemv_kr(W, count) : p.tmk ? 0 : bgemm_kr(W, count, batch, p.nc);
+  p.ncb = p.gemv ? 1 : (batch + 16 * p.nc - 1) / (16 * p.nc);
+  p.kr = p.gemv ? gemv_kr(W, count) : bgemm_kr(W, count, batch, p.nc);
   p.kc = p.kr >= 32 ? 16 : 8;
   {
     const int kc = env_int("TRELLIS_GEMV_KC", 0);
     if (p.gemv && (kc == 8 || kc == 16) && kc <= p.kr) p.kc = kc;
   }
-  auto items = [&](int ks) {
-    long long t = 0;
-    for (int i = 0; i < count; ++i)
-      t += static_cast<long long>((W[i]->n_out + 127) / 128) * ((W[i]->k_in / 16 + ks - 1) / ks);
-    return t;
-  };
-  const int forced = env_int("TRELLIS_TMK_KS", 0);
-  const int target = env_int("TRELLIS_TMK_TARGET", 256);
-  if (forced == 4 || forced == 8 || forced == 16 || forced == 32)
-    p.ks = forced;
-  else
-    p.ks = items(32) >= target ? 32 : items(16) >= target ? 16 : 8;
-  // a k-slice holds whole in-dim Hadamard blocks (the batch-1 path folds x per slice)
-  int bmax = 16;
-  for (int i = 0; i < count; ++i) bmax = W[i]->block_in > bmax ? W[i]->block_in : bmax;
-  while ((p.ks * 16) % bmax) p.ks *= 2;
   p.total = 0;
   p.folds = 0;
   p.ws = 0;
-  const int ncb = p.gemv || p.tmk ? 1 : p.ncb;
-  const int part_cols = p.gemv ? 1 : p.tmk ? p.nb : 16 * p.nc;
+  const int part_cols = p.gemv ? 1 : 16 * p.nc;
   for (int i = 0; i < count; ++i) {
     p.n_ob[i] = (W[i]->n_out + 127) / 128;
-    const int span = p.tmk ? p.ks : p.kr;
-    p.S[i] = (W[i]->k_in / 16 + span - 1) / span;
-    p.total += p.n_ob[i] * ncb * p.S[i];
+    p.S[i] = (W[i]->k_in / 16 + p.kr - 1) / p.kr;
+    p.total += p.n_ob[i] * p.ncb * p.S[i];
     p.folds += p.nb * ((W[i]->k_in + 127) / 128);
     p.off_tickets[i] = p.ws;
     if (p.S[i] > 1) {
-      p.ws += align256(static_cast<size_t>(p.n_ob[i]) * ncb * 4);
+      p.ws += align256(static_cast<size_t>(p.n_ob[i]) * p.ncb * 4);
       p.off_part[i] = p.ws;
-      p.ws += align256(static_cast<size_t>(p.n_ob[i]) * ncb * p.S[i] * part_cols * 128 *
+      p.ws += align256(static_cast<size_t>(p.n_ob[i]) * p.ncb * p.S[i] * part_cols * 128 *
                        sizeof(float));
     } else {
       p.off_part[i] = p.ws;
@@ -240,17 +217,17 @@ GroupPlan group_plan(const trellis_desc* const* W, int count, int batch) {
   return p;
 }
 
-// Batch 1: the wave-pipelined decode-GEMV (its x fold is fused).
-int launch_gemv(int K, int cb, int kc, const TmkArgs& g, hipStream_t st) {
+// Batch 1: the pipelined decode-GEMV (its x fold is fused).
+int launch_gemv(int K, int cb, int V, int kc, const LinArgs& g, hipStream_t st) {
   switch (K) {
-    case 2: return launch_gemv_k<2>(cb, kc, g, st);
-    case 3: return launch_gemv_k<3>(cb, kc, g, st);
-    default: return launch_gemv_k<4>(cb, kc, g, st);
+    case 2: return launch_gemv_k<2>(cb, V, kc, g, st);
+    case 3: return launch_gemv_k<3>(cb, V, kc, g, st);
+    default: return launch_gemv_k<4>(cb, V, kc, g, st);
   }
 }
 
 // The x fold of every member (batch > 1), written once to the workspace.
-int launch_xfold(TmkArgs& g, int folds, hipStream_t st) {
+int launch_xfold(LinArgs& g, int folds, hipStream_t st) {
   const int items = g.total;
   g.total = folds;
   hipLaunchKernelGGL(xfold_kernel, dim3(static_cast<unsigned>((folds + 3) / 4)), dim3(256), 0, st, g);
@@ -259,60 +236,55 @@ int launch_xfold(TmkArgs& g, int folds, hipStream_t st) {
 }
 
 // Batch >= 2: the x fold, the decode-once batched kernel, and (split-K) its reduction.
-int launch_bgemm(int K, int cb, int nc, TmkArgs& g, int folds, int nfold, hipStream_t st) {
+int launch_bgemm(int K, int cb, int V, int nc, LinArgs& g, int folds, int nfold, hipStream_t st) {
   int v = launch_xfold(g, folds, st);
   if (v) return v;
   switch (K) {
-    case 2: v = launch_bgemm_k<2>(cb, nc, g, st); break;
-    case 3: v = launch_bgemm_k<3>(cb, nc, g, st); break;
-    default: v = launch_bgemm_k<4>(cb, nc, g, st); break;
+    case 2: v = launch_bgemm_k<2>(cb, V, nc, g, st); break;
+    case 3: v = launch_bgemm_k<3>(cb, V, nc, g, st); break;
+    default: v = launch_bgemm_k<4>(cb, V, nc, g, st); break;
   }
   if (v || nfold == 0) return v;
   return launch_bfold(cb, nc, nfold, g, st);
 }
 
-// The x fold of every member, then the decode-matmul.
-int launch_tmk(int K, int cb, int ks, TmkArgs& g, int folds, hipStream_t st) {
-  if (g.batch > 1) {
-    const int v = launch_xfold(g, folds, st);
-    if (v) return v;
-  }
-  switch (K) {
-    case 2: return launch_tmk_k<2>(cb, ks, g, st);
-    case 3: return launch_tmk_k<3>(cb, ks, g, st);
-    default: return launch_tmk_k<4>(cb, ks, g, st);
-  }
-}
-
 int validate_group(const trellis_desc* const* W, int count) {
   if (!W || count < 1) return TRELLIS_ERR_NULL;
-  if (count > TMK_MAX_GROUP) return TRELLIS_ERR_GROUP;
+  if (count > MAX_GROUP) return TRELLIS_ERR_GROUP;
   for (int i = 0; i < count; ++i) {
     int v = validate(W[i]);
     if (v) return v;
     v = validate_fold(W[i]);
     if (v) return v;
-    if (W[i]->K != W[0]->K || W[i]->codebook != W[0]->codebook) return TRELLIS_ERR_GROUP;
+    if (W[i]->K != W[0]->K || W[i]->codebook != W[0]->codebook || W[i]->V != W[0]->V)
+      return TRELLIS_ERR_GROUP;
   }
   return TRELLIS_OK;
 }
 
-template <int K>
-int launch_decode_k(int cb, const uint32_t* bits, uint32_t t0, uint32_t nt, float* out,
-                    hipStream_t st) {
+template <int K, int V>
+int launch_decode_kv(int cb, const uint32_t* bits, uint32_t t0, uint32_t nt, float* out,
+                     hipStream_t st) {
   const dim3 grid((nt + 3) / 4);
   switch (cb) {
     case CB_MCG:
-      hipLaunchKernelGGL((decode_tiles_kernel<K, CB_MCG>), grid, dim3(256), 0, st, bits, t0, nt, out);
+      hipLaunchKernelGGL((decode_tiles_kernel<K, CB_MCG, V>), grid, dim3(256), 0, st, bits, t0, nt, out);
       break;
     case CB_3INST:
-      hipLaunchKernelGGL((decode_tiles_kernel<K, CB_3INST>), grid, dim3(256), 0, st, bits, t0, nt, out);
+      hipLaunchKernelGGL((decode_tiles_kernel<K, CB_3INST, V>), grid, dim3(256), 0, st, bits, t0, nt, out);
       break;
     default:
-      hipLaunchKernelGGL((decode_tiles_kernel<K, CB_1MAD>), grid, dim3(256), 0, st, bits, t0, nt, out);
+      hipLaunchKernelGGL((decode_tiles_kernel<K, CB_1MAD, V>), grid, dim3(256), 0, st, bits, t0, nt, out);
       break;
   }
   return hipGetLastError() == hipSuccess ? TRELLIS_OK : TRELLIS_ERR_LAUNCH;
+}
+
+template <int K>
+int launch_decode_k(int cb, int V, const uint32_t* bits, uint32_t t0, uint32_t nt, float* out,
+                    hipStream_t st) {
+  return V == 2 ? launch_decode_kv<K, 2>(cb, bits, t0, nt, out, st)
+                : launch_decode_kv<K, 1>(cb, bits, t0, nt, out, st);
 }
 
 }  // namespace
@@ -331,7 +303,7 @@ const char* trellis_strerror(int status) {
     case TRELLIS_ERR_SHAPE: return "n_out and k_in must be positive multiples of 16";
     case TRELLIS_ERR_BLOCK: return "Hadamard block must be a power of 2 in [16,128] dividing its dim";
     case TRELLIS_ERR_K: return "bits per weight K must be 2, 3 or 4";
-    case TRELLIS_ERR_V: return "only V=1 is supported";
+    case TRELLIS_ERR_V: return "V (weights per trellis step) must be 1 or 2";
     case TRELLIS_ERR_CODEBOOK: return "unknown codebook id";
     case TRELLIS_ERR_NWORDS: return "nwords must equal 256*K/32";
     case TRELLIS_ERR_ALIGN: return "bits must be 16-byte aligned and strides must cover a row";
@@ -340,7 +312,7 @@ const char* trellis_strerror(int status) {
     case TRELLIS_ERR_BATCH: return "batch must be >= 1";
     case TRELLIS_ERR_RANGE: return "tile range outside the matrix";
     case TRELLIS_ERR_LAUNCH: return "HIP kernel launch failed";
-    case TRELLIS_ERR_GROUP: return "a group holds 1..8 linears sharing K and codebook";
+    case TRELLIS_ERR_GROUP: return "a group holds 1..8 linears sharing K, V and codebook";
     default: return "unknown trellis status";
   }
 }
@@ -374,9 +346,9 @@ int trellis_decode_tiles(const trellis_desc* W, uint32_t tile_begin, uint32_t nt
   if (ntiles == 0) return TRELLIS_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (W->K) {
-    case 2: return launch_decode_k<2>(W->codebook, W->bits, tile_begin, ntiles, out, st);
-    case 3: return launch_decode_k<3>(W->codebook, W->bits, tile_begin, ntiles, out, st);
-    default: return launch_decode_k<4>(W->codebook, W->bits, tile_begin, ntiles, out, st);
+    case 2: return launch_decode_k<2>(W->codebook, W->V, W->bits, tile_begin, ntiles, out, st);
+    case 3: return launch_decode_k<3>(W->codebook, W->V, W->bits, tile_begin, ntiles, out, st);
+    default: return launch_decode_k<4>(W->codebook, W->V, W->bits, tile_begin, ntiles, out, st);
   }
 }
 
@@ -403,7 +375,7 @@ int trellis_packed_linear_group(const trellis_desc* const* W, int count, const v
   if (reinterpret_cast<uintptr_t>(workspace) % 256) return TRELLIS_ERR_ALIGN;
   hipStream_t st = static_cast<hipStream_t>(stream);
 
-  TmkArgs g;
+  LinArgs g;
   std::memset(&g, 0, sizeof(g));
   g.nmat = count;
   g.total = p.total;
@@ -414,7 +386,7 @@ int trellis_packed_linear_group(const trellis_desc* const* W, int count, const v
   int item0 = 0;
   char* ws = static_cast<char*>(workspace);
   for (int i = 0; i < count; ++i) {
-    TmkMat& m = g.m[i];
+    LinMat& m = g.m[i];
     m.bits = W[i]->bits;
     m.su = W[i]->su;
     m.sv = W[i]->sv;
@@ -430,7 +402,7 @@ int trellis_packed_linear_group(const trellis_desc* const* W, int count, const v
     m.n_ob = p.n_ob[i];
     m.S = p.S[i];
     m.item0 = item0;
-    item0 += p.n_ob[i] * (p.gemv || p.tmk ? 1 : p.ncb) * p.S[i];
+    item0 += p.n_ob[i] * p.ncb * p.S[i];
     m.tickets = reinterpret_cast<unsigned*>(ws + p.off_tickets[i]);
     m.part = reinterpret_cast<float*>(ws + p.off_part[i]);
     m.xf = reinterpret_cast<uint32_t*>(ws + p.off_xf[i]);
@@ -441,12 +413,12 @@ int trellis_packed_linear_group(const trellis_desc* const* W, int count, const v
   int nfold = 0;
   for (int i = 0; i < count; ++i) {
     g.m[i].fold0 = nfold;
-    if (!p.gemv && !p.tmk && p.S[i] > 1) nfold += p.n_ob[i] * p.ncb;
+    if (!p.gemv && p.S[i] > 1) nfold += p.n_ob[i] * p.ncb;
   }
   if (env_int("TRELLIS_PLAN_LOG", 0))
     std::fprintf(stderr, "trellis plan: batch=%d members=%d mode=%s kr=%d kc=%d nc=%d ncb=%d "
                          "items=%d S0=%d ws=%zu\n",
-                 batch, count, p.gemv ? "gemv" : p.tmk ? "tmk" : "bgemm", p.kr, p.kc, p.nc,
+                 batch, count, p.gemv ? "gemv" : "bgemm", p.kr, p.kc, p.nc,
                  p.ncb, p.total, p.S[0], p.ws);
   const size_t xes = g.x_f16 ? 2 : 4, yes = g.y_f16 ? 2 : 4;
   for (int b0 = 0; b0 < batch; b0 += p.nb) {
@@ -458,9 +430,8 @@ int trellis_packed_linear_group(const trellis_desc* const* W, int count, const v
       g.m[i].chunk0 = chunk0;
       chunk0 += g.batch * ((W[i]->k_in + 127) / 128);
     }
-    v = p.gemv  ? launch_gemv(W[0]->K, W[0]->codebook, p.kc, g, st)
-        : p.tmk ? launch_tmk(W[0]->K, W[0]->codebook, p.ks, g, chunk0, st)
-                : launch_bgemm(W[0]->K, W[0]->codebook, p.nc, g, chunk0, nfold, st);
+    v = p.gemv ? launch_gemv(W[0]->K, W[0]->codebook, W[0]->V, p.kc, g, st)
+               : launch_bgemm(W[0]->K, W[0]->codebook, W[0]->V, p.nc, g, chunk0, nfold, st);
     if (v) return v;
   }
   return TRELLIS_OK;

@@ -84,6 +84,8 @@ class PackedRecord:
         nt = self.tiles_out * self.tiles_in
         if self.bits.shape != (nt, (256 * self.K + 31) // 32):
             raise ValueError(f"bits shape {self.bits.shape} != ({nt}, {(256 * self.K + 31) // 32})")
+        if self.V not in (1, 2):
+            raise ValueError(f"V={self.V}: weights per trellis step must be 1 or 2")
         for nm, arr, ln in (("su", self.su, self.k_in), ("isc", self.isc, self.k_in),
                             ("sv", self.sv, self.n_out), ("osc", self.osc, self.n_out)):
             if arr.shape != (ln,):
