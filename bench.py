@@ -1,17 +1,21 @@
-"""Benchmark: trellis packed-linear decode-GEMV on MI355X, Qwen3-8B block at batch 1.
+"""Benchmark: trellis packed-linear decode-matmul on MI355X, Qwen3-8B block linears.
 
-Workload: the seven linears of one Qwen3-8B decoder block,
+Headline: the seven linears of one Qwen3-8B decoder block,
 q 4096->4096, k/v 4096->1024, o 4096->4096, gate/up 4096->12288, down 12288->4096, K=3,
-MCG, packed bits uniform random from a seed, seeded +-1 signs, per-matrix scale, fp16
-N(0,1) activations. One step = the seven packed linears of one block in forward order as four launches
-(q/k/v grouped, o, gate/up grouped, down). Weights are
-resident in HBM; to defeat the 256 MB Infinity Cache the steps rotate over `copies`
-distinct blocks (>= 1 GB of packed bits by default).
+MCG, V=1, packed bits uniform random from a seed, seeded +-1 signs, per-matrix scale,
+fp16 N(0,1) activations, batch 1. One step = the seven packed linears of one block in
+forward order as four launches (q/k/v grouped, o, gate/up grouped, down: o waits for
+attention and down for the MLP activation in a real forward pass). Weights are resident in
+HBM; to defeat the 256 MB Infinity Cache the steps rotate over `copies` distinct blocks
+(>= 1 GB of packed bits). Each copy's four launches are one HIP graph; steps replay them.
 
 value = packed-weight bytes of the block / seconds per step (GB/s, algorithmic bytes
-n*k*K/8). The JSON line also carries us/layer, the dominant kernel's roofline from HIP
-events on the launch stream, and a CPU baseline: this repo's torch-CPU restatement of
-the reference decode+restore+matmul (oracle/torch_cpu.py) timed on a bounded sample.
+n*k*K/8). The JSON line also carries us/layer, the dominant launch's HBM roofline (gate+up,
+duration from HIP events on the launch stream), the same block at batch 64 with its fp16
+MFMA roofline (algorithmic 2*B*n*k flops), and a CPU baseline: this repo's torch-CPU
+restatement of the reference decode+restore+matmul (oracle/torch_cpu.py) on a bounded
+sample. --sweep adds BASELINE configs[4]: K=2,3,4 x V=1,2 on the gate/up/down shapes at
+batch 1 and at a 512-token prefill.
 """
 from __future__ import annotations
 
@@ -29,13 +33,17 @@ sys.path.insert(0, ROOT)
 
 LAYERS = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
           ("gate", 12288, 4096), ("up", 12288, 4096), ("down", 4096, 12288)]
-# launches of one block in forward order: linears that share an input run as one group
-# (trellis_packed_linear_group); o waits for attention and down for the MLP activation
 GROUPS = [("qkv", ("q", "k", "v")), ("o", ("o",)), ("gate_up", ("gate", "up")),
           ("down", ("down",))]
-DOMINANT = "gate_up"   # 2 x 18,874,368 packed bytes per launch
+DOMINANT = "gate_up"   # 2 x 18,874,368 packed bytes per launch at K=3
+MLP = [("gate", 12288, 4096), ("up", 12288, 4096), ("down", 4096, 12288)]
 HBM_PEAK_GBS = 8000.0
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "tmk_gate_up_b1_traffic.txt")
+MFMA_FP16_PEAK_TFLOPS = 2500.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_gate_up_b1_traffic.txt")
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
 
 
 def traffic_from_profile(path=TRAFFIC_FILE):
@@ -57,12 +65,13 @@ def traffic_from_profile(path=TRAFFIC_FILE):
     return int(round((fetch + write) * 1024))
 
 
-def make_block(te, torch, dev, K, seed, codebook="mcg"):
+def make_layers(te, torch, dev, layers, K, V, seed, codebook="mcg"):
+    """Seeded synthetic packed linears on the device."""
     import numpy as np
     from_dev = te.PackedLinear.from_device
     g = torch.Generator(device=dev)
-    block = {}
-    for i, (name, n, k) in enumerate(LAYERS):
+    out = {}
+    for i, (name, n, k) in enumerate(layers):
         g.manual_seed(seed * 100 + i)
         nt = (n // 16) * (k // 16)
         nw = 256 * K // 32
@@ -77,9 +86,87 @@ def make_block(te, torch, dev, K, seed, codebook="mcg"):
         isc = torch.from_numpy((isc / isc.mean()).astype(np.float16).astype(np.float32) *
                                np.float32(scale)).to(dev)
         osc = torch.from_numpy((osc / osc.mean()).astype(np.float16).astype(np.float32)).to(dev)
-        block[name] = from_dev(n, k, K, bits, su, sv, isc, osc, scale=scale, codebook=codebook,
-                               name=name)
-    return block
+        out[name] = from_dev(n, k, K, bits, su, sv, isc, osc, scale=scale, codebook=codebook,
+                             V=V, name=name)
+    return out
+
+
+def capture(torch, fn):
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    with torch.cuda.graph(g):
+        fn()
+    return g
+
+
+def run_block(te, torch, dev, layers, groups, B, K, V, steps, warmup, min_bytes=1.0e9,
+              per_launch=True):
+    """Time `steps` replays of the block (its launches in order) over distinct weight copies.
+    Returns (seconds per step, {group: us per launch}, {layer: us per launch})."""
+    block_bytes = sum(n * k * K // 8 for _, n, k in layers)
+    copies = max(2, math.ceil(min_bytes / block_bytes))
+    blocks = [make_layers(te, torch, dev, layers, K, V, seed=c) for c in range(copies)]
+    kin = {name: k for name, _, k in layers}
+    xs = {name: torch.randn((B, kin[name]), device=dev, dtype=torch.float16) for name, _, _ in layers}
+    for gname, members in groups:            # members of a group share one input
+        for m in members[1:]:
+            xs[m] = xs[members[0]]
+    ys = {name: torch.empty((B, n), device=dev, dtype=torch.float32) for name, n, _ in layers}
+    grps = [[(gname, te.PackedGroup([blk[m] for m in members]), members)
+             for gname, members in groups] for blk in blocks]
+
+    def step(c, only=None):
+        for gname, grp, members in grps[c % copies]:
+            if only is None or gname == only:
+                grp.forward([xs[m] for m in members], [ys[m] for m in members])
+
+    def single(c, name):
+        blocks[c % copies][name].forward(xs[name], out=ys[name])
+
+    for c in range(copies):            # allocates every workspace once, before capture
+        step(c)
+        for name, _, _ in layers:
+            single(c, name)
+    torch.cuda.synchronize()
+    graphs = [capture(torch, lambda c=c: step(c)) for c in range(copies)]
+    for s in range(warmup):
+        graphs[s % copies].replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(steps):
+        graphs[s % copies].replay()
+    torch.cuda.synchronize()
+    sec = (time.perf_counter() - t0) / steps
+
+    us_group, us_layer = {}, {}
+    if per_launch:
+        reps = max(2, steps // copies)
+
+        def per_launch_us(fn_for_copy):
+            # one graph holding the launch for every copy (distinct weights back to back),
+            # HIP events on the launch stream around its replays
+            g = capture(torch, lambda: [fn_for_copy(c) for c in range(copies)])
+            g.replay()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) * 1e3 / (reps * copies)
+
+        us_group = {gname: round(per_launch_us(lambda c, gname=gname: step(c, gname)), 3)
+                    for gname, _ in groups}
+        us_layer = {name: round(per_launch_us(lambda c, name=name: single(c, name)), 3)
+                    for name, _, _ in layers}
+    del graphs, grps, blocks
+    torch.cuda.empty_cache()
+    return sec, us_group, us_layer, copies
 
 
 def cpu_baseline(budget_s: float = 20.0):
@@ -121,14 +208,20 @@ def cpu_baseline(budget_s: float = 20.0):
             "ms_per_layer": round(med * 1e3, 2)}
 
 
+def block_flops(layers, B):
+    return sum(2 * B * n * k for _, n, k in layers)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--batch", type=int, default=1, help="headline batch (BASELINE: 1)")
     ap.add_argument("--K", type=int, default=3)
-    ap.add_argument("--copies", type=int, default=0, help="distinct weight blocks (0: >= 1 GB)")
+    ap.add_argument("--V", type=int, default=1)
+    ap.add_argument("--no-batch64", action="store_true", help="skip the batch-64 MFMA figure")
+    ap.add_argument("--sweep", action="store_true", help="add BASELINE configs[4] (K x V sweep)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     args = ap.parse_args()
@@ -142,86 +235,60 @@ def main():
     te = importlib.import_module("trellis-everywhere_amd")
     te.library()
     dev = torch.device("cuda:0")
-    block_bytes = sum(n * k * args.K // 8 for _, n, k in LAYERS)
-    copies = args.copies or max(1, math.ceil(1.0e9 / block_bytes))
-    blocks = [make_block(te, torch, dev, args.K, seed=c) for c in range(copies)]
-    B = args.batch
-    xs = {name: torch.randn((B, k), device=dev, dtype=torch.float16) for name, _, k in LAYERS}
-    # group members that share an input read the same tensor
-    xs["k"] = xs["v"] = xs["q"]
-    xs["up"] = xs["gate"]
-    ys = {name: torch.empty((B, n), device=dev, dtype=torch.float32) for name, n, _ in LAYERS}
-    groups = [[(gname, te.PackedGroup([blk[m] for m in members]), members)
-               for gname, members in GROUPS] for blk in blocks]
-    for blk, grps in zip(blocks, groups):
-        for lin in blk.values():
-            lin._workspace(B)
-        for _, grp, _ in grps:
-            grp._workspace(B)
+    B, K, V = args.batch, args.K, args.V
+    block_bytes = sum(n * k * K // 8 for _, n, k in LAYERS)
 
-    def step(s, only=None):
-        for gname, grp, members in groups[s % copies]:
-            if only is None or gname == only:
-                grp.forward([xs[m] for m in members], [ys[m] for m in members])
-
-    def single(s, name):
-        blocks[s % copies][name].forward(xs[name], out=ys[name])
-
-    # warm up eagerly (allocates nothing later), then capture one HIP graph per weight
-    # copy: the four launches of a block replay without per-call host overhead
-    for s in range(max(args.warmup, copies)):
-        step(s)
-        for name, _, _ in LAYERS:
-            single(s, name)
-    torch.cuda.synchronize()
-
-    def capture(fn):
-        g = torch.cuda.CUDAGraph()
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
-            fn()
-        torch.cuda.current_stream().wait_stream(side)
-        with torch.cuda.graph(g):
-            fn()
-        return g
-
-    graphs = [capture(lambda c=c: step(c)) for c in range(copies)]
-    for s in range(args.warmup):
-        graphs[s % copies].replay()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for s in range(args.steps):
-        graphs[s % copies].replay()
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    sec_per_step = (t1 - t0) / args.steps
-
-    # launch durations from HIP events on the launch stream: one graph holding a
-    # launch for every weight copy (distinct weights back to back), events around its
-    # replays; average = elapsed / launches
-    reps = max(1, args.steps // copies)
-
-    def per_launch_us(fn_for_copy):
-        g = capture(lambda: [fn_for_copy(c) for c in range(copies)])
-        g.replay()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
-            g.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) * 1e3 / (reps * copies)
-
-    us_layer = {name: round(per_launch_us(lambda c, name=name: single(c, name)), 3)
-                for name, _, _ in LAYERS}
-    us_group = {gname: round(per_launch_us(lambda c, gname=gname: step(c, gname)), 3)
-                for gname, _ in GROUPS}
+    log(f"[bench] block batch {B} K={K} V={V}")
+    sec, us_group, us_layer, copies = run_block(te, torch, dev, LAYERS, GROUPS, B, K, V,
+                                                args.steps, args.warmup)
+    gbs = block_bytes / sec / 1e9
     dom_us = us_group[DOMINANT]
-    dom_bytes = 2 * 12288 * 4096 * args.K // 8
+    dom_bytes = 2 * 12288 * 4096 * K // 8
     achieved = dom_bytes / (dom_us * 1e-6) / 1e9
-    gbs = block_bytes / sec_per_step / 1e9
+    log(f"[bench] {sec * 1e6:.2f} us/block, {gbs:.1f} GB/s; groups {us_group}")
+
+    batch64 = None
+    if not args.no_batch64 and B == 1:
+        log("[bench] block batch 64")
+        s64, g64, _, _ = run_block(te, torch, dev, LAYERS, GROUPS, 64, K, V,
+                                   max(20, args.steps // 10), max(3, args.warmup // 5),
+                                   per_launch=True)
+        fl = block_flops(LAYERS, 64)
+        dom_fl = 2 * 64 * 2 * 12288 * 4096
+        dom_tf = dom_fl / (g64[DOMINANT] * 1e-6) / 1e12
+        batch64 = {"us_per_block": round(s64 * 1e6, 2),
+                   "tflops": round(fl / s64 / 1e12, 2),
+                   "mfma_frac_of_fp16_peak": round(fl / s64 / 1e12 / MFMA_FP16_PEAK_TFLOPS, 4),
+                   "us_per_group_launch": g64,
+                   "roofline": {"bound": "mfma", "achieved": round(dom_tf, 2),
+                                "peak": MFMA_FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                "frac": round(dom_tf / MFMA_FP16_PEAK_TFLOPS, 4),
+                                "kernel": "bgemm_kernel<K=3,MCG,V=1,NC=4> (+xfold, bfold) on "
+                                          "gate+up at batch 64",
+                                "avg_launch_us": g64[DOMINANT],
+                                "algorithmic_flops_per_launch": dom_fl}}
+        log(f"[bench] batch 64: {batch64['us_per_block']} us/block, {batch64['tflops']} TFLOP/s")
+
+    sweep = None
+    if args.sweep:
+        sweep = []
+        for Ks in (2, 3, 4):
+            for Vs in (1, 2):
+                for Bs in (1, 512):
+                    log(f"[bench] sweep K={Ks} V={Vs} batch={Bs}")
+                    steps = args.steps if Bs == 1 else max(10, args.steps // 20)
+                    ssec, sg, _, _ = run_block(te, torch, dev, MLP,
+                                               [(n, (n,)) for n, _, _ in MLP], Bs, Ks, Vs,
+                                               steps, max(2, args.warmup // 5),
+                                               per_launch=True)
+                    pb = sum(n * k * Ks // 8 for _, n, k in MLP)
+                    fl = block_flops(MLP, Bs)
+                    sweep.append({"K": Ks, "V": Vs, "batch": Bs,
+                                  "us_gate_up_down": round(ssec * 1e6, 2),
+                                  "us_per_layer": sg,
+                                  "packed_GBps": round(pb / ssec / 1e9, 1),
+                                  "pct_of_hbm_peak": round(100 * pb / ssec / 1e9 / HBM_PEAK_GBS, 2),
+                                  "tflops": round(fl / ssec / 1e12, 2)})
 
     # known-size copy for the HBM-counter scale factor (FETCH_SIZE / WRITE_SIZE)
     src = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
@@ -237,34 +304,37 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(sec_per_step * 1e3, 4),
+        "ms_per_step": round(sec * 1e3, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "u32 packed K=3 trellis, fp16 activations, fp32 accumulate",
+        "dtype": f"u32 packed K={K} trellis (V={V}), fp16 activations, fp32 accumulate",
         "data": "synthetic: uniform random packed bits, seeded signs/scales, fp16 N(0,1) x",
-        "config": {"workload": "Qwen3-8B decoder-block linears (q,k,v,o,gate,up,down), K=3, "
-                               "MCG, batch %d" % B,
-                   "batch": B, "K": args.K, "codebook": "mcg",
+        "config": {"workload": f"Qwen3-8B decoder-block linears (q,k,v,o,gate,up,down), K={K}, "
+                               f"MCG, V={V}, batch {B}",
+                   "batch": B, "K": K, "V": V, "codebook": "mcg",
                    "block_packed_bytes": block_bytes, "weight_copies": copies,
                    "rotated_bytes": block_bytes * copies,
                    "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
-                   "us_per_block": round(sec_per_step * 1e6, 2),
+                   "us_per_block": round(sec * 1e6, 2),
                    "launches_per_block": [g for g, _ in GROUPS],
                    "us_per_group_launch": us_group,
-                   "us_per_layer_single_launch": us_layer},
+                   "us_per_layer_single_launch": us_layer,
+                   "batch64": batch64,
+                   "sweep_configs4": sweep},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic_from_profile() if args.batch == 1 and args.K == 3
-                     else None,
-                     "traffic_source": "profiles/tmk_gate_up_b1_traffic.txt (rocprofv3 "
+                     "traffic": traffic_from_profile() if B == 1 and K == 3 and V == 1 else None,
+                     "traffic_source": "profiles/gemv_gate_up_b1_traffic.txt (rocprofv3 "
                                        "FETCH_SIZE/WRITE_SIZE, copy-scaled)",
-                     "kernel": "tmk_kernel<K=3,MCG,KS,XB=1> on the gate+up group "
-                               "(2 x 12288x4096, one launch)",
+                     "kernel": f"gemv_kernel<K={K},MCG,V={V}> on the gate+up group "
+                               "(2 x 12288x4096, one launch)" if B == 1 else
+                               f"bgemm_kernel<K={K},MCG,V={V}> on the gate+up group",
                      "avg_launch_us": round(dom_us, 3),
                      "algorithmic_bytes_per_launch": dom_bytes},
     }
     if not args.no_cpu_baseline:
+        log("[bench] cpu baseline")
         out["cpu_baseline"] = cpu_baseline(args.cpu_budget)
     print(json.dumps(out), flush=True)
 
