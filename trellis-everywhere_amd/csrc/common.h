@@ -39,6 +39,7 @@ struct LinMat {
   long long ldx, ldy;
   int n, k, tiles_in, block_in, block_out;
   int n_ob, S;
+  unsigned s_inv;       // ceil(2^32 / S) for S > 1 (item / S = umulhi(item, s_inv)), else 0
   int item0;            // first group-wide work item of this matrix
   int chunk0;           // first group-wide x-fold job of this matrix
   int fold0;            // first group-wide bfold_kernel workgroup of this matrix
@@ -54,6 +55,16 @@ struct LinArgs {
   int kr;               // tile columns per k-range
 };
 
+// Range-checked buffer loads: a buffer resource over [base, base + bytes); an offset at or
+// past the end reads zeros without touching memory. Word 3 is gfx9's raw-buffer format.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes),
+                                           0x00020000);
+}
+constexpr unsigned RSRC_OOB = 0x40000000u;   // an offset past every buffer made here
+constexpr int AUX_NT = 2;                    // nontemporal cache policy (gfx94x/gfx950)
+
 // Activation i of an f16 or f32 array, read as the aligned u32 word holding it so the
 // load is branch-free (f16 arrays must be 4-byte aligned with an even row stride).
 __device__ __forceinline__ uint32_t load_act_word(const void* p, long long i, int is_f16) {
@@ -67,16 +78,55 @@ __device__ __forceinline__ float act_value(uint32_t w, long long i, int is_f16) 
   return static_cast<float>(__builtin_bit_cast(_Float16, h));
 }
 
-// Butterflies of a normalized-free block Hadamard (block B <= 128) on a 128-element
-// chunk held as lo = e[lane], hi = e[lane + 64].
-__device__ __forceinline__ void fwht_chunk(float& lo, float& hi, int B, int lane) {
-  for (int h = 1; h < B && h < 64; h <<= 1) {
-    const float plo = __shfl_xor(lo, h);
-    const float phi = __shfl_xor(hi, h);
-    const bool upper = (lane & h) != 0;
-    lo = upper ? plo - lo : lo + plo;
-    hi = upper ? phi - hi : hi + phi;
+// The value lane ^ H holds, without LDS: DPP for partners inside a 16-lane row
+// (quad_perm for 1 and 2; row rotations for 4 and 8, where row_ror:N hands lane i the value
+// of lane i - N within its row) and gfx950's permlane swaps for 16 and 32 (with both
+// operands equal, the first result holds the partner of the odd rows / upper half, the
+// second that of the even rows / lower half).
+template <int H>
+__device__ __forceinline__ float lane_xor(float v, int lane) {
+  const int iv = __builtin_bit_cast(int, v);
+  int r;
+  if constexpr (H == 1) {
+    r = __builtin_amdgcn_mov_dpp(iv, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+  } else if constexpr (H == 2) {
+    r = __builtin_amdgcn_mov_dpp(iv, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+  } else if constexpr (H == 4) {
+    const int dn = __builtin_amdgcn_mov_dpp(iv, 0x124, 0xF, 0xF, false);  // lane i - 4
+    const int up = __builtin_amdgcn_mov_dpp(iv, 0x12C, 0xF, 0xF, false);  // lane i + 4
+    r = (lane & 4) ? dn : up;
+  } else if constexpr (H == 8) {
+    r = __builtin_amdgcn_mov_dpp(iv, 0x128, 0xF, 0xF, false);  // row_ror:8 = lane i ^ 8
+  } else if constexpr (H == 16) {
+    const auto p = __builtin_amdgcn_permlane16_swap(iv, iv, false, false);
+    r = (lane & 16) ? static_cast<int>(p[0]) : static_cast<int>(p[1]);
+  } else {
+    static_assert(H == 32, "partner distance");
+    const auto p = __builtin_amdgcn_permlane32_swap(iv, iv, false, false);
+    r = (lane & 32) ? static_cast<int>(p[0]) : static_cast<int>(p[1]);
   }
+  return __builtin_bit_cast(float, r);
+}
+
+template <int H>
+__device__ __forceinline__ void butterfly(float& lo, float& hi, int lane) {
+  const float plo = lane_xor<H>(lo, lane);
+  const float phi = lane_xor<H>(hi, lane);
+  const bool upper = (lane & H) != 0;
+  lo = upper ? plo - lo : lo + plo;
+  hi = upper ? phi - hi : hi + phi;
+}
+
+// Butterflies of a normalized-free block Hadamard (block B <= 128, a power of 2) on a
+// 128-element chunk held as lo = e[lane], hi = e[lane + 64]; pairs are exchanged in
+// registers (lane_xor), so a level costs a few VALU operations, not an LDS round trip.
+__device__ __forceinline__ void fwht_chunk(float& lo, float& hi, int B, int lane) {
+  if (B > 1) butterfly<1>(lo, hi, lane);
+  if (B > 2) butterfly<2>(lo, hi, lane);
+  if (B > 4) butterfly<4>(lo, hi, lane);
+  if (B > 8) butterfly<8>(lo, hi, lane);
+  if (B > 16) butterfly<16>(lo, hi, lane);
+  if (B > 32) butterfly<32>(lo, hi, lane);
   if (B == 128) {
     const float a = lo, b = hi;
     lo = a + b;

@@ -39,16 +39,24 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
   constexpr int CH = SW / 4;                 // 16-byte chunks per wave-stage
   constexpr int LOADS = (CH + 63) / 64;      // chunks per lane
   constexpr int CPT = NWK / 4;               // chunks per tile
+  constexpr int SWP = LOADS * 256;           // words per wave buffer: every lane's chunks
   constexpr int FCH = GEMV_MAX_KR * 16 / 128 / GEMV_WAVES;  // fold chunks per wave (max)
-  __shared__ __align__(16) uint32_t stg[GEMV_WAVES * SW];
+  __shared__ __align__(16) uint32_t stg[GEMV_WAVES * SWP];
   __shared__ __align__(16) uint32_t xs[GEMV_MAX_KR * 16];
   __shared__ float tt[2][128];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __shared__ unsigned ready[GEMV_MAX_KR / 8];   // per 128-column chunk of xs: folded
+  __shared__ unsigned nready;                    // chunks folded so far
+  // the wave index is uniform: kept scalar, so per-wave choices are scalar branches
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (threadIdx.x < GEMV_MAX_KR / 8) ready[threadIdx.x] = 0u;
+  if (threadIdx.x == 0) nready = 0u;
+  __syncthreads();
   const int bl = wave & 7, half = wave >> 3;     // band of the block, half of the k-range
   const int mi = locate_mat(g, blockIdx.x, false);
   const LinMat& m = g.m[mi];
-  const int local = blockIdx.x - m.item0;
-  const int ob = local / m.S, sl = local % m.S;
+  const unsigned local = blockIdx.x - m.item0;
+  const int ob = m.S > 1 ? static_cast<int>(__umulhi(local, m.s_inv)) : static_cast<int>(local);
+  const int sl = static_cast<int>(local) - ob * m.S;
   const int c0 = sl * g.kr;                          // first tile column of the k-range
   const int ntl = min(g.kr, m.tiles_in - c0);        // tile columns in the k-range
   const int nst = (ntl + KC - 1) / KC;
@@ -56,51 +64,68 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
   const int s_begin = half ? s_mid : 0, s_end = half ? nst : s_mid;
   const int rows = min(128, m.n - ob * 128);
   const int band = ob * 8 + min(bl, rows / 16 - 1);
-  const uint32_t* bsrc = m.bits + (static_cast<size_t>(band) * m.tiles_in + c0) * NWK;
-  uint32_t* mystg = stg + wave * SW;
-
-  // ---- output scales of this block for the fold (wave 0), activation loads of the
-  // k-range fold (chunk w and w + GEMV_WAVES per wave), then the first packed words: the
-  // fold and the epilogue never wait behind the packed-word stream
-  float so[2] = {0.f, 0.f};
-  if (wave == 0) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int row = ob * 128 + min(lane + 64 * h, rows - 1);
-      so[h] = m.sv[row] * m.osc[row];
-    }
-  }
+  uint32_t* mystg = stg + wave * SWP;
   const int kcols = ntl * 16;
   const int nch = (kcols + 127) / 128;
+
+  // ---- loads. All of them go through range-checked buffer resources: an index past the
+  // block's rows, the k-range's columns or the band's tiles reads zeros without touching
+  // memory, so no address is clamped, every load is issued on every path (the number in
+  // flight is static and each wait covers only the loads it needs), and per-lane offsets
+  // are fixed while the per-stage part is one add. Order: output scales of the block
+  // (used at the end), the fold's inputs (chunks w and w + GEMV_WAVES of the k-range),
+  // then the first PF stages of packed words.
+  const rsrc_t r_sv = make_rsrc(m.sv + ob * 128, rows * 4);
+  const rsrc_t r_osc = make_rsrc(m.osc + ob * 128, rows * 4);
+  const int xsh = g.x_f16 ? 1 : 2;                   // log2 bytes per activation
+  const rsrc_t r_x = make_rsrc(static_cast<const char*>(m.x) + (static_cast<size_t>(c0) * 16 << xsh),
+                               static_cast<unsigned>(kcols) << xsh);
+  const rsrc_t r_su = make_rsrc(m.su + c0 * 16, kcols * 4);
+  const rsrc_t r_isc = make_rsrc(m.isc + c0 * 16, kcols * 4);
+  const rsrc_t r_bits = make_rsrc(m.bits + (static_cast<size_t>(band) * m.tiles_in + c0) * NWK,
+                                  static_cast<unsigned>(ntl) * NWK * 4);
+  float so[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int o = (lane + 64 * h) * 4;
+    so[h] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r_sv, o, 0, 0)) *
+            __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r_osc, o, 0, 0));
+  }
   uint32_t fw[FCH][2];
-  float fsc[FCH][2];
+  float fsu[FCH][2], fis[FCH][2];
 #pragma unroll
   for (int f = 0; f < FCH; ++f) {
     const int ch = wave + GEMV_WAVES * f;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const int i = c0 * 16 + min(ch * 128 + lane + 64 * h, kcols - 1);
-      if (ch < nch) {
-        fw[f][h] = load_act_word(m.x, i, g.x_f16);
-        fsc[f][h] = m.su[i] * m.isc[i];
-      }
+      const unsigned e = ch < nch ? ch * 128 + lane + 64 * h : RSRC_OOB / 4;
+      fw[f][h] = __builtin_amdgcn_raw_buffer_load_b32(r_x, static_cast<int>(((e << xsh) & ~3u)), 0, 0);
+      fsu[f][h] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r_su, static_cast<int>(e * 4), 0, 0));
+      fis[f][h] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r_isc, static_cast<int>(e * 4), 0, 0));
     }
   }
+  // keeps the fold's loads ahead of the packed words in issue order
+  asm volatile("" ::: "memory");
+  // byte offset of this lane's 16-byte chunk within a stage (chunks past the stage's last
+  // are pointed out of range), and of stage s within the band's k-range
   u32x4_t R[PF][LOADS];
-  auto load_stage = [&](int s, u32x4_t (&dst)[LOADS]) {
+  unsigned lo_q[LOADS];
 #pragma unroll
-    for (int q = 0; q < LOADS; ++q) {
-      const int ch = lane + 64 * q;
-      if (CH % 64 == 0 || ch < CH) {
-        const int t = min(s * KC + ch / CPT, ntl - 1);
-        dst[q] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4_t*>(bsrc + static_cast<size_t>(t) * NWK) + ch % CPT);
-      }
-    }
+  for (int q = 0; q < LOADS; ++q) {
+    const int ch = lane + 64 * q;
+    lo_q[q] = CH % 64 == 0 || ch < CH ? static_cast<unsigned>(((ch / CPT) * NWK + 4 * (ch % CPT)) * 4)
+                                      : RSRC_OOB;
+  }
+  auto load_stage = [&](int s, u32x4_t (&dst)[LOADS]) {
+    // a stage past the wave's last one (prefetch beyond the end) reads nothing
+    const unsigned soff = s < s_end ? static_cast<unsigned>(s * KC * NWK * 4) : RSRC_OOB;
+#pragma unroll
+    for (int q = 0; q < LOADS; ++q)
+      dst[q] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                               r_bits, static_cast<int>(lo_q[q] + soff), 0, AUX_NT));
   };
 #pragma unroll
-  for (int b = 0; b < PF; ++b)
-    if (s_begin + b < s_end) load_stage(s_begin + b, R[b]);
+  for (int b = 0; b < PF; ++b) load_stage(s_begin + b, R[b]);
 
   // ---- activation fold: xf = Hb_k(isc_scaled * su * x) / sqrt(block_in) as (x,x) pairs
   {
@@ -110,15 +135,40 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
       const int ch = wave + GEMV_WAVES * f;
       if (ch < nch) {
         const int e0 = ch * 128 + lane, e1 = e0 + 64;
-        float lo = e0 < kcols ? act_value(fw[f][0], c0 * 16 + e0, g.x_f16) * fsc[f][0] : 0.0f;
-        float hi = e1 < kcols ? act_value(fw[f][1], c0 * 16 + e1, g.x_f16) * fsc[f][1] : 0.0f;
+        // columns past the k-range loaded as zeros
+        float lo = act_value(fw[f][0], e0, g.x_f16) * (fsu[f][0] * fis[f][0]);
+        float hi = act_value(fw[f][1], e1, g.x_f16) * (fsu[f][1] * fis[f][1]);
         fwht_chunk(lo, hi, m.block_in, lane);
         xs[e0] = dup_half(lo * nrm);
         xs[e1] = dup_half(hi * nrm);
+        // publish the chunk: its xs words are written before the flag
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        if (lane == 0) {
+          __hip_atomic_store(&ready[ch], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          __hip_atomic_fetch_add(&nready, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
       }
     }
   }
-  __syncthreads();
+  // No barrier: a wave decodes a stage as soon as the chunks it covers are folded (each
+  // wait ends: every chunk's folding wave publishes it before it decodes anything); once
+  // a wave has seen every chunk folded it stops checking.
+  bool all_ready = false;
+  auto wait_chunks = [&](int s) {
+    if (all_ready || s >= s_end) return;
+    const unsigned done = __builtin_amdgcn_readfirstlane(
+        __hip_atomic_load(&nready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+    if (done >= static_cast<unsigned>(nch)) {
+      all_ready = true;
+    } else {
+      const int ca = (s * KC) >> 3, cb = min((s * KC + KC - 1) >> 3, nch - 1);
+      for (int c = ca; c <= cb; ++c)
+        while (__builtin_amdgcn_readfirstlane(__hip_atomic_load(
+                   &ready[c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) == 0u)
+          __builtin_amdgcn_s_sleep(1);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  };
 
   // ---- main loop: stage s is moved from registers to the wave's LDS buffer, the load
   // of stage s + PF is issued into the freed registers, then stage s is decoded
@@ -127,12 +177,12 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
   float4_t acc = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
   half8_t Bv[GEMV_G];
   auto stage = [&](int s, u32x4_t (&src)[LOADS]) {
+    // lanes past the stage's last chunk write the buffer's padding: no masked region
 #pragma unroll
-    for (int q = 0; q < LOADS; ++q) {
-      const int ch = lane + 64 * q;
-      if (CH % 64 == 0 || ch < CH) *reinterpret_cast<u32x4_t*>(mystg + 4 * ch) = src[q];
-    }
-    if (s + PF < s_end) load_stage(s + PF, src);
+    for (int q = 0; q < LOADS; ++q)
+      *reinterpret_cast<u32x4_t*>(mystg + 4 * (lane + 64 * q)) = src[q];
+    load_stage(s + PF, src);
+    wait_chunks(s);
     const uint32_t* xst = xs + s * KC * 16 + 4 * gq;
     // G tiles at a time: their LDS reads, then their decodes into separate A registers,
     // then their MFMAs on alternating accumulators, so a decode never waits for the
@@ -159,7 +209,8 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
           acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[j], Bv[j], acc, 0, 0, 0);
       }
     };
-    const int jn = ntl - s * KC;
+    // tiles of this stage: none past the wave's last stage
+    const int jn = s < s_end ? ntl - s * KC : 0;
     if (jn >= KC) {
 #pragma unroll
       for (int j0 = 0; j0 < KC; j0 += GEMV_G) group(j0);
@@ -172,14 +223,14 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
       }
     }
   };
+  // PF stages per trip, all of them issued (a stage past s_end decodes nothing), so the
+  // register ring keeps a fixed shape
   for (int s = s_begin; s < s_end; s += PF) {
 #pragma unroll
-    for (int b = 0; b < PF; ++b) {
-      if (s + b < s_end) {
-        stage(s + b, R[b]);
-      }
-    }
+    for (int b = 0; b < PF; ++b) stage(s + b, R[b]);
   }
+  // the ring's last loads (stages past the end) are not consumed: let them land
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   acc += acc1;
   // column 0 of C: lanes 0, 16, 32, 48 hold rows 4*gq + i of the band
   if (r == 0) {

@@ -401,6 +401,8 @@ int trellis_packed_linear_group(const trellis_desc* const* W, int count, const v
     m.block_out = W[i]->block_out;
     m.n_ob = p.n_ob[i];
     m.S = p.S[i];
+    // exact for item * S < 2^32: items < 2^20 and S <= 256 here
+    m.s_inv = p.S[i] > 1 ? static_cast<unsigned>((0x100000000ULL + p.S[i] - 1) / p.S[i]) : 0u;
     m.item0 = item0;
     item0 += p.n_ob[i] * p.ncb * p.S[i];
     m.tickets = reinterpret_cast<unsigned*>(ws + p.off_tickets[i]);
