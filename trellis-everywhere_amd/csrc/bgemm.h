@@ -31,7 +31,7 @@ template <int CB>
 __device__ __forceinline__ void bg_out_fold(const LinArgs& g, const LinMat& m, const float* tl,
                                             int ob, int b0, int nbv, int rows) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const float nrm = 1.0f / sqrtf(static_cast<float>(m.block_out));
+  const float nrm = m.nrm_out;
   float so[2];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {

@@ -38,6 +38,7 @@ struct LinMat {
   unsigned* tickets;    // workspace: [n_ob] arrival counters (batch 1, S > 1), zero between calls
   long long ldx, ldy;
   int n, k, tiles_in, block_in, block_out;
+  float nrm_in, nrm_out;  // 1 / sqrt(block_in), 1 / sqrt(block_out), rounded as fp32 ops
   int n_ob, S;
   unsigned s_inv;       // ceil(2^32 / S) for S > 1 (item / S = umulhi(item, s_inv)), else 0
   int item0;            // first group-wide work item of this matrix
@@ -179,7 +180,7 @@ __global__ __launch_bounds__(256) void xfold_kernel(LinArgs g) {
   float lo = e0 < kvalid ? act_value(w0, x0i, g.x_f16) * s0 : 0.0f;
   float hi = e1 < kvalid ? act_value(w1, x1i, g.x_f16) * s1 : 0.0f;
   fwht_chunk(lo, hi, m.block_in, lane);
-  const float nrm = 1.0f / sqrtf(static_cast<float>(m.block_in));
+  const float nrm = m.nrm_in;
   uint32_t* dst = m.xf + static_cast<size_t>(b) * m.k + ch * 128;
   if (e0 < kvalid) dst[e0] = dup_half(lo * nrm);
   if (e1 < kvalid) dst[e1] = dup_half(hi * nrm);

@@ -124,12 +124,14 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
       dst[q] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
                                                r_bits, static_cast<int>(lo_q[q] + soff), 0, AUX_NT));
   };
-#pragma unroll
-  for (int b = 0; b < PF; ++b) load_stage(s_begin + b, R[b]);
+  // only the first stage before the fold: a smaller burst of loads at kernel start, so
+  // every wave's first stage (and the fold's inputs) arrive sooner; the rest of the
+  // ring follows the fold
+  load_stage(s_begin, R[0]);
 
   // ---- activation fold: xf = Hb_k(isc_scaled * su * x) / sqrt(block_in) as (x,x) pairs
   {
-    const float nrm = 1.0f / sqrtf(static_cast<float>(m.block_in));
+    const float nrm = m.nrm_in;
 #pragma unroll
     for (int f = 0; f < FCH; ++f) {
       const int ch = wave + GEMV_WAVES * f;
@@ -150,6 +152,8 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
       }
     }
   }
+#pragma unroll
+  for (int b = 1; b < PF; ++b) load_stage(s_begin + b, R[b]);
   // No barrier: a wave decodes a stage as soon as the chunks it covers are folded (each
   // wait ends: every chunk's folding wave publishes it before it decodes anything); once
   // a wave has seen every chunk folded it stops checking.
@@ -279,7 +283,7 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
     t1 = t1 / 147.800537109375f;
   }
   fwht_chunk(t0, t1, m.block_out, lane);
-  const float nrm = 1.0f / sqrtf(static_cast<float>(m.block_out));
+  const float nrm = m.nrm_out;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int rl = lane + 64 * h;

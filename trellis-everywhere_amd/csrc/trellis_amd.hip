@@ -3,6 +3,7 @@
 // batch 1, xfold_kernel + bgemm_kernel (+ bfold_kernel) above).
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -399,6 +400,9 @@ int trellis_packed_linear_group(const trellis_desc* const* W, int count, const v
     m.tiles_in = W[i]->k_in / 16;
     m.block_in = W[i]->block_in;
     m.block_out = W[i]->block_out;
+    // the same correctly rounded fp32 sqrt and divide the kernels would do
+    m.nrm_in = 1.0f / std::sqrt(static_cast<float>(W[i]->block_in));
+    m.nrm_out = 1.0f / std::sqrt(static_cast<float>(W[i]->block_out));
     m.n_ob = p.n_ob[i];
     m.S = p.S[i];
     // exact for item * S < 2^32: items < 2^20 and S <= 256 here
