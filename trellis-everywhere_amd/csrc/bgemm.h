@@ -1,24 +1,31 @@
 // bgemm.h — batched packed linear for gfx950 (batch 2 .. prefill): decode once, reuse
 // across the batch.
 //
-// A workgroup (4 waves) owns one 128-row output block (the out-dim Hadamard block; wave w
-// owns bands 2w and 2w+1) x NB = 16*NC batch columns x one k-range of `kr` tile columns,
-// walked in steps of KT tiles (8, or 4 at 128 columns):
-//   * step s+1 is loaded into registers (the B tile: xf[batch cols][64] as (x, x) fp16
-//     pairs written by xfold_kernel; the waves' packed words) while step s is computed,
-//     then stored to the other half of a double-buffered LDS area; one barrier per step;
+// A workgroup of 16 waves owns one 128-row output block (the out-dim Hadamard block) x
+// NB = 16*NC batch columns x one k-range of `kr` tile columns, walked in steps of KT tiles
+// (8, or 4 at 128 columns). Wave w = (band pair bp = w % 4, k-lane kl = w / 4): the four
+// waves of a SIMD share band pair bp (bands 2bp, 2bp+1) and split every step's tiles
+// between them (tile j of a step belongs to k-lane j % 4), so a SIMD always has four
+// waves to switch between:
+//   * the B tile of a step (xf[batch cols][KT*16] as (x, x) fp16 pairs written by
+//     xfold_kernel) is loaded two steps ahead into registers by all 1024 threads, stored
+//     to one half of a double-buffered LDS area, and read by every wave: each fragment
+//     serves the 2 bands of each of the 4 band pairs; one barrier per step;
+//   * each wave's packed words ride a two-step register ring and a wave-private LDS
+//     buffer (for the lanes' window reads), as in gemv_kernel;
 //   * each wave decodes a tile of each of its bands once, straight into the A operand of
 //     v_mfma_f32_16x16x32_f16 (the exact (hi, lo) pair against the duplicated activation,
-//     common.h), and issues NC MFMAs per band against the NC batch chunks, so the
-//     decode is amortised over all NB columns and each B fragment read from LDS serves
-//     both bands;
+//     common.h), and issues NC MFMAs per band against the NC batch chunks;
+//   * every load is a range-checked buffer load (batch rows past the call's, tiles past the
+//     matrix read zeros), so none is clamped or skipped and the waits stay exact;
 //   * the B rows are padded by 4 words so the 16 batch rows of a fragment fall in
 //     different LDS banks;
-//   * the epilogue stages t[NB][128] in LDS; with one k-range the workgroup applies
-//     y = sv * osc * Hb_n(t) itself, otherwise it stores its partial block and
-//     bfold_kernel (next launch) adds the slices in slice order (deterministic) and folds:
-//     a cross-CU reduction inside the kernel would wait on device-scope round trips of
-//     ~2 us each, with one workgroup's worth of loads in flight.
+//   * the epilogue adds the four k-lanes' sums into t[NB][128] in LDS in k-lane order
+//     (deterministic); with one k-range the workgroup applies y = sv * osc * Hb_n(t)
+//     itself, otherwise it stores its partial block and bfold_kernel (next launch) adds
+//     the slices in slice order and folds, one wave per batch column: reducing inside the
+//     kernel leaves the whole reduction to the last workgroup of each block, behind
+//     device-scope round trips, and measured slower.
 #pragma once
 
 #include "common.h"
@@ -26,8 +33,9 @@
 namespace trellis {
 
 // y[b0 + b] = sv * osc * Hb_n(t[b]) for the nbv batch columns staged in LDS as
-// t[b][128]; one column per wave at a time (256-thread workgroups).
-template <int CB>
+// t[b][TLS] (rows padded to TLS), summed over NR regions NR_OFF floats apart; one column
+// per wave at a time (WAVES waves).
+template <int CB, int WAVES, int TLS, int NR, int NR_OFF>
 __device__ __forceinline__ void bg_out_fold(const LinArgs& g, const LinMat& m, const float* tl,
                                             int ob, int b0, int nbv, int rows) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -38,9 +46,14 @@ __device__ __forceinline__ void bg_out_fold(const LinArgs& g, const LinMat& m, c
     const int row = ob * 128 + min(lane + 64 * h, rows - 1);
     so[h] = m.sv[row] * m.osc[row] * nrm;
   }
-  for (int b = wave; b < nbv; b += 4) {
-    float lo = lane < rows ? tl[b * 128 + lane] : 0.f;
-    float hi = lane + 64 < rows ? tl[b * 128 + lane + 64] : 0.f;
+  for (int b = wave; b < nbv; b += WAVES) {
+    float lo = tl[b * TLS + lane], hi = tl[b * TLS + lane + 64];
+    if (NR == 2) {
+      lo += tl[NR_OFF + b * TLS + lane];
+      hi += tl[NR_OFF + b * TLS + lane + 64];
+    }
+    if (lane >= rows) lo = 0.f;
+    if (lane + 64 >= rows) hi = 0.f;
     if (CB == CB_1MAD) {
       lo = lo / 147.800537109375f;
       hi = hi / 147.800537109375f;
@@ -63,25 +76,36 @@ __device__ __forceinline__ void bg_out_fold(const LinArgs& g, const LinMat& m, c
 
 // k-step: 8 tile columns for up to 64 batch columns, 4 for 128 (LDS holds two B steps)
 template <int NC> struct BgStep { static constexpr int KT = NC <= 4 ? 8 : 4; };
+constexpr int BG_WAVES = 16;
+constexpr int BG_KL = 4;   // k-lanes: waves of one band pair splitting each step's tiles
 
 template <int K, int CB, int V, int NC>
-__global__ __launch_bounds__(256) void bgemm_kernel(LinArgs g) {
+__global__ __launch_bounds__(64 * BG_WAVES) void bgemm_kernel(LinArgs g) {
   constexpr int NWK = 8 * K;
-  constexpr int BG_KT = BgStep<NC>::KT;            // tile columns per k-step
-  constexpr int BG_XW = BG_KT * 16 + 4;            // LDS words per B row (+4: bank spread)
+  constexpr int KT = BgStep<NC>::KT;               // tile columns per k-step
+  constexpr int TPL = KT / BG_KL;                  // tiles per band per k-lane per step
+  constexpr int XW = KT * 16 + 4;                  // LDS words per B row (+4: bank spread)
   constexpr int NB = 16 * NC;                      // batch columns per workgroup
-  constexpr int RCH = BG_KT * 4;                   // 16-byte chunks per B row per step
+  constexpr int RCH = KT * 4;                      // 16-byte chunks per B row per step
   constexpr int XCH = NB * RCH;                    // 16-byte B chunks per step
-  constexpr int XLOADS = (XCH + 255) / 256;
-  constexpr int BW = 2 * BG_KT * NWK;              // packed words per wave per step
-  constexpr int BCH = BW / 4;                      // 16-byte chunks per wave per step
+  constexpr int XLOADS = (XCH + 64 * BG_WAVES - 1) / (64 * BG_WAVES);
+  constexpr int XBUF = NB * XW;                    // words per B buffer
+  constexpr int CPT = NWK / 4;                     // 16-byte chunks per tile
+  constexpr int BCH = 2 * TPL * CPT;               // 16-byte chunks per wave per step
   constexpr int BLOADS = (BCH + 63) / 64;
-  constexpr int XBUF = NB * BG_XW;                 // words per B buffer
+  constexpr int BSW = BLOADS * 256;                // words per wave buffer: every lane's chunks
+  static_assert(NB * 132 <= 2 * XBUF, "epilogue t[NB][132] reuses the B buffers");
   __shared__ __align__(16) uint32_t xsb[2 * XBUF];
-  __shared__ __align__(16) uint32_t bst[2][4][BW];
-  float* tl = reinterpret_cast<float*>(xsb);       // epilogue: t[NB][128] (fits in 2*XBUF)
+  __shared__ __align__(16) uint32_t bst[BG_WAVES * BSW];
+  // epilogue: t[NB][TLS] (rows padded so a lane group's float4 writes spread over the
+  // banks), in two regions when they fit (k-lanes 0 + 2 and 1 + 3), else one
+  constexpr int TLS = 132;
+  constexpr int NR = 2 * NB * TLS <= 2 * XBUF ? 2 : 1;
+  constexpr int NR_OFF = NB * TLS;
+  float* tl = reinterpret_cast<float*>(xsb);
 
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int bp = wave & 3, kl = wave >> 2;
   const int mi = locate_mat(g, blockIdx.x, false);
   const LinMat& m = g.m[mi];
   const int local = blockIdx.x - m.item0;
@@ -92,47 +116,55 @@ __global__ __launch_bounds__(256) void bgemm_kernel(LinArgs g) {
   const int nbv = min(NB, g.batch - b0);           // valid batch columns
   const int c0 = sl * g.kr;
   const int ntl = min(g.kr, m.tiles_in - c0);
-  const int nsteps = (ntl + BG_KT - 1) / BG_KT;
+  const int nsteps = (ntl + KT - 1) / KT;
   const int rows = min(128, m.n - ob * 128);
+  uint32_t* mystg = bst + wave * BSW;
 
-  u32x4_t xr[XLOADS], br[BLOADS];
-  auto load_step = [&](int s) {
+  // B: rows b0 .. b0 + nbv - 1 of xf (a batch row past the call's reads zeros; columns
+  // past the k-range feed only tiles that are not decoded)
+  const rsrc_t r_x = make_rsrc(m.xf + static_cast<size_t>(b0) * m.k,
+                               static_cast<unsigned>(nbv) * m.k * 4);
+  unsigned xoff[XLOADS];
 #pragma unroll
-    for (int q = 0; q < XLOADS; ++q) {
-      const int ch = threadIdx.x + 256 * q;
-      if (XCH % 256 == 0 || ch < XCH) {
-        const int n = ch / RCH, off = ch % RCH;     // batch row, 16-byte chunk of its row
-        const int col = (c0 + s * BG_KT) * 16 + off * 4;
-        const bool ok = n < nbv && col < (c0 + ntl) * 16;
-        const uint32_t* src = m.xf + static_cast<size_t>(b0 + min(n, nbv - 1)) * m.k +
-                              min(col, m.k - 4);
-        xr[q] = *reinterpret_cast<const u32x4_t*>(src);
-        if (!ok) xr[q] = u32x4_t{0u, 0u, 0u, 0u};
-      }
-    }
+  for (int q = 0; q < XLOADS; ++q) {
+    const int ch = threadIdx.x + 64 * BG_WAVES * q;
+    const int n = ch / RCH, off = ch % RCH;        // batch row, 16-byte chunk of its row
+    xoff[q] = ch < XCH ? static_cast<unsigned>((n * m.k + c0 * 16 + off * 4) * 4) : RSRC_OOB;
+  }
+  // packed words from the block's first band to the end of the matrix (bands past the
+  // matrix read zeros); lane chunk -> (band of the pair, tile of the k-lane, chunk)
+  const size_t blk0 = static_cast<size_t>(ob) * 8 * m.tiles_in * NWK;
+  const rsrc_t r_b = make_rsrc(m.bits + blk0,
+                               static_cast<unsigned>((static_cast<size_t>(m.n / 16) * m.tiles_in * NWK - blk0) * 4));
+  unsigned boff[BLOADS];
 #pragma unroll
-    for (int q = 0; q < BLOADS; ++q) {
-      const int ch = lane + 64 * q;
-      if (BCH % 64 == 0 || ch < BCH) {
-        const int bb = ch / (BCH / 2), rem = ch % (BCH / 2);
-        const int band = ob * 8 + min(2 * wave + bb, rows / 16 - 1);
-        const int tile = c0 + min(s * BG_KT + rem / (NWK / 4), ntl - 1);
-        br[q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(
-            m.bits + (static_cast<size_t>(band) * m.tiles_in + tile) * NWK) + rem % (NWK / 4));
-      }
-    }
+  for (int q = 0; q < BLOADS; ++q) {
+    const int ch = lane + 64 * q;
+    const int bb = ch / (TPL * CPT), rem = ch % (TPL * CPT);
+    const int t = rem / CPT, c = rem % CPT;
+    boff[q] = ch < BCH ? static_cast<unsigned>(((2 * bp + bb) * m.tiles_in + c0 + kl + BG_KL * t) * NWK * 4 + c * 16)
+                       : RSRC_OOB;
+  }
+  u32x4_t xr[2][XLOADS], br[2][BLOADS];
+  auto load_step = [&](int s, u32x4_t (&xd)[XLOADS], u32x4_t (&bd)[BLOADS]) {
+    // a step past the last reads nothing
+    const unsigned sx = s < nsteps ? static_cast<unsigned>(s * KT * 16 * 4) : RSRC_OOB;
+    const unsigned sb = s < nsteps ? static_cast<unsigned>(s * KT * NWK * 4) : RSRC_OOB;
+#pragma unroll
+    for (int q = 0; q < XLOADS; ++q)
+      xd[q] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                              r_x, static_cast<int>(xoff[q] + sx), 0, 0));
+#pragma unroll
+    for (int q = 0; q < BLOADS; ++q)
+      bd[q] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                              r_b, static_cast<int>(boff[q] + sb), 0, AUX_NT));
   };
-  auto store_step = [&](int buf) {
+  auto store_b = [&](int buf, const u32x4_t (&xd)[XLOADS]) {
 #pragma unroll
     for (int q = 0; q < XLOADS; ++q) {
-      const int ch = threadIdx.x + 256 * q;
-      if (XCH % 256 == 0 || ch < XCH)
-        *reinterpret_cast<u32x4_t*>(xsb + buf * XBUF + (ch / RCH) * BG_XW + (ch % RCH) * 4) = xr[q];
-    }
-#pragma unroll
-    for (int q = 0; q < BLOADS; ++q) {
-      const int ch = lane + 64 * q;
-      if (BCH % 64 == 0 || ch < BCH) *reinterpret_cast<u32x4_t*>(&bst[buf][wave][4 * ch]) = br[q];
+      const int ch = threadIdx.x + 64 * BG_WAVES * q;
+      if (XCH % (64 * BG_WAVES) == 0 || ch < XCH)
+        *reinterpret_cast<u32x4_t*>(xsb + buf * XBUF + (ch / RCH) * XW + (ch % RCH) * 4) = xd[q];
     }
   };
 
@@ -144,90 +176,138 @@ __global__ __launch_bounds__(256) void bgemm_kernel(LinArgs g) {
 #pragma unroll
     for (int c = 0; c < NC; ++c) acc[b][c] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-  load_step(0);
-  store_step(0);
+  load_step(0, xr[0], br[0]);
+  load_step(1, xr[1], br[1]);
+  store_b(0, xr[0]);
   __syncthreads();
-  for (int s = 0; s < nsteps; ++s) {
-    const int buf = s & 1;
-    if (s + 1 < nsteps) load_step(s + 1);
-    const uint32_t* xb = xsb + buf * XBUF + r * BG_XW + 4 * gq;
+  // two steps per trip so the register rings keep a fixed shape; a step past the last
+  // computes nothing, and its loads read nothing
+  for (int s = 0; s < nsteps; s += 2) {
 #pragma unroll
-    for (int t = 0; t < BG_KT; ++t) {
-      const uint32_t* t0 = &bst[buf][wave][t * NWK];
-      const uint32_t* t1 = &bst[buf][wave][(BG_KT + t) * NWK];
-      const half8_t A0 = decode_a<K, CB, V>(t0[qp.wa], t0[qp.wb], qp.sh);
-      const half8_t A1 = decode_a<K, CB, V>(t1[qp.wa], t1[qp.wb], qp.sh);
+    for (int h = 0; h < 2; ++h) {
+      const int st = s + h;
+      // this wave's packed words of step st to its LDS buffer, then refill the slot with
+      // step st + 2 (the B part of that slot was stored to LDS one step earlier)
 #pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const half8_t B = __builtin_bit_cast(
-            half8_t, *reinterpret_cast<const u32x4_t*>(xb + c * 16 * BG_XW + t * 16));
-        acc[0][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, B, acc[0][c], 0, 0, 0);
-        acc[1][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, B, acc[1][c], 0, 0, 0);
+      for (int q = 0; q < BLOADS; ++q)
+        *reinterpret_cast<u32x4_t*>(mystg + 4 * (lane + 64 * q)) = br[h][q];
+      load_step(st + 2, xr[h], br[h]);
+      if (st < nsteps) {
+        const uint32_t* xb = xsb + h * XBUF + r * XW + 4 * gq;
+#pragma unroll
+        for (int t = 0; t < TPL; ++t) {
+          const int j = kl + BG_KL * t;            // tile of the step
+          if (st * KT + j < ntl) {
+            const uint32_t* t0 = mystg + t * NWK;
+            const uint32_t* t1 = mystg + (TPL + t) * NWK;
+            const half8_t A0 = decode_a<K, CB, V>(t0[qp.wa], t0[qp.wb], qp.sh);
+            const half8_t A1 = decode_a<K, CB, V>(t1[qp.wa], t1[qp.wb], qp.sh);
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+              const half8_t B = __builtin_bit_cast(
+                  half8_t, *reinterpret_cast<const u32x4_t*>(xb + c * 16 * XW + j * 16));
+              acc[0][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, B, acc[0][c], 0, 0, 0);
+              acc[1][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, B, acc[1][c], 0, 0, 0);
+            }
+          }
+        }
       }
+      // the B tile of step st + 1 (loaded a step ago) to the other buffer; the barrier
+      // also tells every wave that this buffer's step is done
+      store_b(h ^ 1, xr[h ^ 1]);
+      __syncthreads();
     }
-    if (s + 1 < nsteps) store_step(buf ^ 1);
+  }
+  // the rings' last loads (steps past the end) are not consumed: let them land
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  // ---- t[batch col][row] in LDS, k-lanes added in a fixed order: lane (n, gq) of band
+  // b, chunk c holds rows 4gq .. 4gq + 3 (one float4)
+  for (int k2 = 0; k2 < BG_KL; k2 += NR) {
+    if (kl >= k2 && kl < k2 + NR) {
+      float* reg = tl + (kl - k2) * NR_OFF;
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          float4_t* p = reinterpret_cast<float4_t*>(&reg[(c * 16 + r) * TLS + 32 * bp + 16 * b + 4 * gq]);
+          *p = k2 == 0 ? acc[b][c] : *p + acc[b][c];
+        }
+    }
     __syncthreads();
   }
-
-  // ---- t[batch col][row] in LDS: lane (n, gq) of band b, chunk c holds rows 4gq + i
-#pragma unroll
-  for (int b = 0; b < 2; ++b)
-#pragma unroll
-    for (int c = 0; c < NC; ++c)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) tl[(c * 16 + r) * 128 + 32 * wave + 16 * b + 4 * gq + i] = acc[b][c][i];
-  __syncthreads();
 
   if (m.S > 1) {
     // publish this slice's partial block; bfold_kernel adds the slices and folds
     float* mypart = m.part + (static_cast<size_t>(ob * ncb + cb) * m.S + sl) * NB * 128;
-    for (int i = threadIdx.x; i < nbv * 32; i += 256)
-      reinterpret_cast<float4_t*>(mypart)[i] = reinterpret_cast<const float4_t*>(tl)[i];
+    const float4_t* t4 = reinterpret_cast<const float4_t*>(tl);
+    for (int i = threadIdx.x; i < nbv * 32; i += 64 * BG_WAVES) {
+      const int j = (i >> 5) * (TLS / 4) + (i & 31);
+      float4_t v = t4[j];
+      if (NR == 2) v += t4[NR_OFF / 4 + j];
+      reinterpret_cast<float4_t*>(mypart)[i] = v;
+    }
     return;
   }
-  bg_out_fold<CB>(g, m, tl, ob, b0, nbv, rows);
+  bg_out_fold<CB, BG_WAVES, TLS, NR, NR_OFF>(g, m, tl, ob, b0, nbv, rows);
 }
 
-// Split-K reduction of bgemm_kernel: one workgroup per (matrix, 128-row block, column
-// block) adds the S partial blocks in slice order (deterministic), then folds. Runs after
+// Split-K reduction of bgemm_kernel: one wave per (matrix, 128-row block, batch column):
+// it loads that column's 128 rows of every slice at once (S slices x 2 values per lane in
+// flight), adds them in slice order (deterministic), and folds y = sv * osc * Hb_n(t).
+// Workgroup = 4 batch columns of one (matrix, block, column block). Runs after
 // bgemm_kernel, so plain loads see its plain stores.
 template <int CB, int NC>
 __global__ __launch_bounds__(256) void bfold_kernel(LinArgs g) {
-  constexpr int NB = 16 * NC;
-  __shared__ __align__(16) float tl[NB * 128];
-  const int mi = locate_fold(g, blockIdx.x);
+  constexpr int NB = 16 * NC, CG = NB / 4;        // workgroups per (block, column block)
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int fi = blockIdx.x / CG, cg = blockIdx.x % CG;
+  const int mi = locate_fold(g, fi);
   const LinMat& m = g.m[mi];
   const int ncb = (g.batch + NB - 1) / NB;
-  const int local = blockIdx.x - m.fold0;
+  const int local = fi - m.fold0;
   const int ob = local / ncb, cb = local % ncb;
   const int b0 = cb * NB, nbv = min(NB, g.batch - b0);
+  const int n = cg * 4 + wave;                    // batch column of the block
+  if (n >= nbv) return;
   const int rows = min(128, m.n - ob * 128);
-  const float4_t* part = reinterpret_cast<const float4_t*>(
-      m.part + static_cast<size_t>(ob * ncb + cb) * m.S * NB * 128);
-  const size_t stride = static_cast<size_t>(NB) * 32;       // float4s per slice
-  for (int i0 = threadIdx.x; i0 < nbv * 32; i0 += 2 * 256) {
-    float4_t a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
-    const int i1 = min(i0 + 256, nbv * 32 - 1);
-    for (int s0 = 0; s0 < m.S; s0 += 4) {
-      float4_t q0[4], q1[4];
+  const int S = m.S;
+  const float* p = m.part + static_cast<size_t>(ob * ncb + cb) * S * NB * 128 + n * 128;
+  float lo = 0.f, hi = 0.f;
+  for (int s0 = 0; s0 < S; s0 += 8) {
+    float q0[8], q1[8];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const size_t so = static_cast<size_t>(min(s0 + v, m.S - 1)) * stride;
-        q0[v] = part[so + i0];
-        q1[v] = part[so + i1];
-      }
-#pragma unroll
-      for (int v = 0; v < 4; ++v)
-        if (s0 + v < m.S) {
-          a0 += q0[v];
-          a1 += q1[v];
-        }
+    for (int v = 0; v < 8; ++v) {
+      const float* ps = p + static_cast<size_t>(min(s0 + v, S - 1)) * NB * 128;
+      q0[v] = ps[lane];
+      q1[v] = ps[lane + 64];
     }
-    reinterpret_cast<float4_t*>(tl)[i0] = a0;
-    if (i0 + 256 < nbv * 32) reinterpret_cast<float4_t*>(tl)[i0 + 256] = a1;
+#pragma unroll
+    for (int v = 0; v < 8; ++v)
+      if (s0 + v < S) {
+        lo += q0[v];
+        hi += q1[v];
+      }
   }
-  __syncthreads();
-  bg_out_fold<CB>(g, m, tl, ob, b0, nbv, rows);
+  if (CB == CB_1MAD) {
+    lo = lo / 147.800537109375f;
+    hi = hi / 147.800537109375f;
+  }
+  fwht_chunk(lo, hi, m.block_out, lane);
+  const float nrm = m.nrm_out;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int rl = lane + 64 * h;
+    if (rl < rows) {
+      const int row = ob * 128 + rl;
+      const float v = (h ? hi : lo) * (m.sv[row] * m.osc[row] * nrm);
+      const long long o = static_cast<long long>(b0 + n) * m.ldy + row;
+      if (g.y_f16)
+        static_cast<_Float16*>(m.y)[o] = static_cast<_Float16>(v);
+      else
+        static_cast<float*>(m.y)[o] = v;
+    }
+  }
 }
 
 }  // namespace trellis

@@ -43,7 +43,7 @@ struct LinMat {
   unsigned s_inv;       // ceil(2^32 / S) for S > 1 (item / S = umulhi(item, s_inv)), else 0
   int item0;            // first group-wide work item of this matrix
   int chunk0;           // first group-wide x-fold job of this matrix
-  int fold0;            // first group-wide bfold_kernel workgroup of this matrix
+  int fold0;            // first group-wide bfold_kernel job of this matrix
 };
 
 struct LinArgs {

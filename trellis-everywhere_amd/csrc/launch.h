@@ -19,13 +19,14 @@ int launch_gemv_k(int cb, int V, int kc, const LinArgs& g, hipStream_t st);
 template <int K>
 int launch_bgemm_k(int cb, int V, int nc, const LinArgs& g, hipStream_t st);
 
-// bfold_kernel<cb, nc> over nfold workgroups (after a split-K bgemm_kernel).
+// bfold_kernel<cb, nc> over nfold (block, column block) jobs of 4 * nc workgroups each
+// (after a split-K bgemm_kernel).
 int launch_bfold(int cb, int nc, int nfold, const LinArgs& g, hipStream_t st);
 
 #ifdef TRELLIS_BFOLD_DEFINE
 template <int CB>
 static int launch_bfold_cb(int nc, int nfold, const LinArgs& g, hipStream_t st) {
-  const dim3 grid(static_cast<unsigned>(nfold));
+  const dim3 grid(static_cast<unsigned>(nfold * 4 * nc));
   switch (nc) {
     case 1: hipLaunchKernelGGL((bfold_kernel<CB, 1>), grid, dim3(256), 0, st, g); break;
     case 2: hipLaunchKernelGGL((bfold_kernel<CB, 2>), grid, dim3(256), 0, st, g); break;
@@ -73,10 +74,10 @@ template <int K, int CB, int V>
 static int launch_bgemm_nc(int nc, const LinArgs& g, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(g.total));
   switch (nc) {
-    case 1: hipLaunchKernelGGL((bgemm_kernel<K, CB, V, 1>), grid, dim3(256), 0, st, g); break;
-    case 2: hipLaunchKernelGGL((bgemm_kernel<K, CB, V, 2>), grid, dim3(256), 0, st, g); break;
-    case 4: hipLaunchKernelGGL((bgemm_kernel<K, CB, V, 4>), grid, dim3(256), 0, st, g); break;
-    default: hipLaunchKernelGGL((bgemm_kernel<K, CB, V, 8>), grid, dim3(256), 0, st, g); break;
+    case 1: hipLaunchKernelGGL((bgemm_kernel<K, CB, V, 1>), grid, dim3(64 * BG_WAVES), 0, st, g); break;
+    case 2: hipLaunchKernelGGL((bgemm_kernel<K, CB, V, 2>), grid, dim3(64 * BG_WAVES), 0, st, g); break;
+    case 4: hipLaunchKernelGGL((bgemm_kernel<K, CB, V, 4>), grid, dim3(64 * BG_WAVES), 0, st, g); break;
+    default: hipLaunchKernelGGL((bgemm_kernel<K, CB, V, 8>), grid, dim3(64 * BG_WAVES), 0, st, g); break;
   }
   return hipGetLastError() == hipSuccess ? 0 : 13;
 }

@@ -137,12 +137,11 @@ int gemv_kr(const trellis_desc* const* W, int count) {
 
 // Batch >= 2 (bgemm_kernel): NC 16-column batch chunks per workgroup (up to 128 columns),
 // a work item is one 128-row block x one column block x one k-range of kr tile columns
-// (a multiple of the k-step, 8 tiles up to 64 columns, else 4). A workgroup has one wave
-// per SIMD, so a CU needs two or three resident workgroups to hide latency: kr minimises
-// ceil(items/CUs) x the per-wave work of an item (2 bands x kr tiles x (decode ~61 + NC
-// MFMAs x ~19 cycles)) divided by an occupancy efficiency (0.4 / 0.7 / 1 for 1 / 2 / >= 3
-// resident workgroups, the residency capped by LDS and registers), plus, with split-K, the
-// bfold_kernel launch that adds the S partial blocks and folds. At most 8 slices.
+// (a multiple of the k-step, 8 tiles up to 64 columns, else 4), run by one 16-wave
+// workgroup per CU. kr minimises ceil(items/CUs) x the per-SIMD work of an item (2 bands
+// x kr tiles x (decode ~61 + NC MFMAs x ~19 cycles)) plus, with split-K, the bfold_kernel
+// launch (~1.5 us) and the partial blocks it moves (S x rows x NB x 4 bytes written and
+// read at ~2.5 KB per cycle), plus a start-up latency per round after the first.
 // TRELLIS_BGEMM_KR forces a value.
 int bgemm_nc(int batch) { return batch <= 16 ? 1 : batch <= 32 ? 2 : batch <= 64 ? 4 : 8; }
 
@@ -158,22 +157,19 @@ int bgemm_kr(const trellis_desc* const* W, int count, int batch, int nc) {
   int best = cap;
   long long best_cost = -1;
   for (int kr = kt; kr <= cap; kr += kt) {
-    long long items = 0;
+    long long items = 0, part_bytes = 0;
     int smax = 1;
     for (int i = 0; i < count; ++i) {
       const int S = (W[i]->k_in / 16 + kr - 1) / kr;
-      items += static_cast<long long>((W[i]->n_out + 127) / 128) * ncb * S;
+      const long long n_ob = (W[i]->n_out + 127) / 128;
+      items += n_ob * ncb * S;
       smax = S > smax ? S : smax;
+      if (S > 1) part_bytes += static_cast<long long>(S) * n_ob * ncb * 128 * 16 * nc * 4;
     }
-    if (smax > 8) continue;
-    const long long ipc = (items + cus - 1) / cus;
-    const long long rmax = nc == 1 ? 6 : nc == 2 ? 4 : nc == 4 ? 2 : 2;
-    const long long res = ipc < rmax ? ipc : rmax;
-    const long long eff10 = res >= 3 ? 10 : res == 2 ? 7 : 4;
-    // split-K: one more launch (~1.5 us) that reads smax partial blocks of 16*nc x 128
-    // floats per (block, column block) at ~64 bytes per cycle per CU
-    const long long epi = smax > 1 ? 3600 + 1200 + smax * 16 * nc * 128 * 4 / 64 : 0;
-    const long long cost = ipc * kr * 2 * (61 + 19 * nc) * 10 / eff10 + epi;
+    if (smax > 16) continue;
+    const long long rounds = (items + cus - 1) / cus;
+    const long long epi = smax > 1 ? 3600 + 2 * part_bytes / 2500 : 0;
+    const long long cost = rounds * kr * 2 * (61 + 19 * nc) + epi + (rounds - 1) * 3600;
     if (best_cost < 0 || cost < best_cost) {
       best = kr;
       best_cost = cost;
@@ -415,7 +411,7 @@ int trellis_packed_linear_group(const trellis_desc* const* W, int count, const v
   }
   // the members' item ranges must tile the grid exactly
   if (item0 != p.total) return TRELLIS_ERR_LAUNCH;
-  // bfold_kernel workgroups: one per (block, column block) of every split-K member
+  // bfold_kernel jobs: one per (block, column block) of every split-K member
   int nfold = 0;
   for (int i = 0; i < count; ++i) {
     g.m[i].fold0 = nfold;
