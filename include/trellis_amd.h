@@ -118,6 +118,15 @@ int trellis_packed_linear_group(const trellis_desc *const *W, int count, const v
 int trellis_decode_tiles(const trellis_desc *W, uint32_t tile_begin, uint32_t ntiles,
                          float *out, void *stream);
 
+/* Embedding rows with the full restore: out[t, :] = W_hat[tokens[t], :] for t < ntok.
+ * Replaces PackedOps.embedRow / DECODE_EMBED (web/packed.js:137-146,
+ * web/kernels.js:192-249), which decodes one token per dispatch; here ntok tokens per call.
+ *   tokens: device int32 [ntok]; an id outside [0, n_out) yields a row of zeros
+ *   out: [ntok, k_in] with row stride ldo elements, dtype out_dtype (f16 or f32)
+ * Each token decodes the block_out x k_in weights of its row's Hadamard block once. */
+int trellis_embed_rows(const trellis_desc *W, const int32_t *tokens, int ntok, void *out,
+                       int64_t ldo, int out_dtype, void *stream);
+
 /* Human-readable name of a status code. */
 const char *trellis_strerror(int status);
 

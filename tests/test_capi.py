@@ -66,6 +66,21 @@ def test_packed_linear_rejects_before_launch(te):
     assert lib.trellis_decode_tiles(ctypes.byref(d), 100, 100, 16, None) == 12
 
 
+def test_embed_rows_rejects_before_launch(te):
+    """trellis_embed_rows validates on the host: descriptor, token count, pointers, dtype
+    and row stride (web/packed.js:137-146 has no error path)."""
+    lib = te.library()
+    d = _desc(te)
+    assert lib.trellis_embed_rows(ctypes.byref(_desc(te, K=5, nwords=40)), 16, 1, 16, 256, 0,
+                                  None) == 4
+    assert lib.trellis_embed_rows(ctypes.byref(d), 16, -1, 16, 256, 0, None) == 11
+    assert lib.trellis_embed_rows(ctypes.byref(d), 16, 0, None, 256, 0, None) == 0
+    assert lib.trellis_embed_rows(ctypes.byref(d), None, 2, 16, 256, 0, None) == 1
+    assert lib.trellis_embed_rows(ctypes.byref(d), 16, 2, None, 256, 0, None) == 1
+    assert lib.trellis_embed_rows(ctypes.byref(d), 16, 2, 16, 256, 7, None) == 9
+    assert lib.trellis_embed_rows(ctypes.byref(d), 16, 2, 16, 255, 0, None) == 8
+
+
 def test_workspace_plan_is_bounded(te):
     """Workspace for the largest BASELINE shape stays small (partials of 128-row blocks)."""
     lib = te.library()

@@ -1,0 +1,116 @@
+// embed.h — embedding-row lookup from a packed trellis matrix with the full restore:
+// out[t, j] = W_hat[tok[t], j] (web/kernels.js:192-249 DECODE_EMBED, web/packed.js:137-146).
+//
+// W_hat[r, j] = sv[r] osc[r] su[j] isc_scaled[j] / sqrt(B_n B_k)
+//               * sum_l H_k[j % B_k, l] * sum_c H_n[r % B_n, c] * zq[rb + c, jb + l]
+// (rb, jb: first row / column of r's and j's Hadamard blocks; H entries (-1)^popcount(a&b)).
+// The two Hadamard sums commute, so every weight of the B_n x B_k block is decoded once
+// per (token, column block): one workgroup per (token, column block), 4 waves.
+//   * wave w takes the bands b = w, w + 4, ... of the row block; lane (row rl = l%16,
+//     column group g = l/16) decodes 4 weights of each tile (the same window/codebook
+//     code as the matmul kernels, exact fp32 values) and accumulates sign(rr, 16b + rl)
+//     * w per column, so a lane holds 4 columns of each of the block's tile columns;
+//   * the 16 rows of a lane group are summed by DPP butterflies (all-reduce within a
+//     16-lane row), the 4 waves' column sums are added in LDS in wave order;
+//   * wave 0 applies the column-side Hadamard (fwht_chunk) and the scales.
+// A token id outside [0, n_out) yields a row of zeros.
+#pragma once
+
+#include "common.h"
+
+namespace trellis {
+
+struct EmbedArgs {
+  const uint32_t* bits;
+  const float* su;
+  const float* sv;
+  const float* isc;     // isc_scaled = f32(isc) * scale
+  const float* osc;
+  const int32_t* tokens;
+  void* out;
+  long long ldo;
+  int n, k, tiles_in, block_in, block_out, nblk;   // nblk = k / block_in
+  float nrm;            // 1/sqrt(block_in) * 1/sqrt(block_out), fp32
+  int out_f16;
+};
+
+template <int K, int CB, int V>
+__global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
+  constexpr int NWK = 8 * K;
+  __shared__ float colsum[4][128];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int t = blockIdx.x / a.nblk, jblk = blockIdx.x % a.nblk;
+  const int jb = jblk * a.block_in;                 // first column of the block
+  const int tok = a.tokens[t];
+  const bool ok = tok >= 0 && tok < a.n;
+  const int r = ok ? tok : 0;
+  const int rb = r - r % a.block_out, rr = r % a.block_out;
+  const int ntc = a.block_in / 16, nbands = a.block_out / 16;
+  const int rl = lane & 15, g = lane >> 4;
+  const QuadPos qp = quad_pos_v<K, V>(rl, g);
+
+  float acc[8][4];
+#pragma unroll
+  for (int tc = 0; tc < 8; ++tc)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) acc[tc][q] = 0.f;
+  for (int b = wave; b < nbands; b += 4) {
+    const int c = 16 * b + rl;                       // row within the row block
+    const float sgn = (__builtin_popcount(rr & c) & 1) ? -1.f : 1.f;
+    const uint32_t* band = a.bits + (static_cast<size_t>(rb / 16 + b) * a.tiles_in + jb / 16) * NWK;
+#pragma unroll
+    for (int tc = 0; tc < 8; ++tc) {
+      if (tc < ntc) {
+        const uint32_t* tp = band + tc * NWK;
+        uint32_t raw[4];
+        decode_quad<K, CB, V>(tp[qp.wa], tp[qp.wb], qp.sh, raw);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[tc][q] += sgn * cb_exact<CB>(raw[q]);
+      }
+    }
+  }
+  // sum over the 16 rows of each lane group (a 16-lane DPP row)
+#pragma unroll
+  for (int tc = 0; tc < 8; ++tc)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float v = acc[tc][q];
+      v += lane_xor<1>(v, lane);
+      v += lane_xor<2>(v, lane);
+      v += lane_xor<4>(v, lane);
+      v += lane_xor<8>(v, lane);
+      acc[tc][q] = v;
+    }
+  if (rl == 0) {
+#pragma unroll
+    for (int tc = 0; tc < 8; ++tc)
+      if (tc < ntc)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) colsum[wave][16 * tc + 4 * g + q] = acc[tc][q];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  float lo = 0.f, hi = 0.f;
+  const int nw = nbands < 4 ? nbands : 4;
+  for (int w = 0; w < nw; ++w) {
+    if (lane < a.block_in) lo += colsum[w][lane];
+    if (lane + 64 < a.block_in) hi += colsum[w][lane + 64];
+  }
+  fwht_chunk(lo, hi, a.block_in, lane);
+  const float rs = ok ? a.sv[r] * a.osc[r] * a.nrm : 0.f;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int jl = lane + 64 * h;
+    if (jl < a.block_in) {
+      const int j = jb + jl;
+      const float v = (h ? hi : lo) * rs * a.isc[j] * a.su[j];
+      const long long o = static_cast<long long>(t) * a.ldo + j;
+      if (a.out_f16)
+        static_cast<_Float16*>(a.out)[o] = static_cast<_Float16>(v);
+      else
+        static_cast<float*>(a.out)[o] = v;
+    }
+  }
+}
+
+}  // namespace trellis

@@ -13,6 +13,7 @@
 #define TRELLIS_XFOLD_DEFINE
 #define TRELLIS_BFOLD_DEFINE
 #include "launch.h"
+#include "embed.h"
 
 using namespace trellis;
 
@@ -284,6 +285,21 @@ int launch_decode_k(int cb, int V, const uint32_t* bits, uint32_t t0, uint32_t n
                 : launch_decode_kv<K, 1>(cb, bits, t0, nt, out, st);
 }
 
+template <int K, int V>
+int launch_embed_kv(int cb, const EmbedArgs& a, unsigned grid, hipStream_t st) {
+  switch (cb) {
+    case CB_MCG: hipLaunchKernelGGL((embed_kernel<K, CB_MCG, V>), dim3(grid), dim3(256), 0, st, a); break;
+    case CB_3INST: hipLaunchKernelGGL((embed_kernel<K, CB_3INST, V>), dim3(grid), dim3(256), 0, st, a); break;
+    default: hipLaunchKernelGGL((embed_kernel<K, CB_1MAD, V>), dim3(grid), dim3(256), 0, st, a); break;
+  }
+  return hipGetLastError() == hipSuccess ? TRELLIS_OK : TRELLIS_ERR_LAUNCH;
+}
+
+template <int K>
+int launch_embed_k(int cb, int V, const EmbedArgs& a, unsigned grid, hipStream_t st) {
+  return V == 2 ? launch_embed_kv<K, 2>(cb, a, grid, st) : launch_embed_kv<K, 1>(cb, a, grid, st);
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------- C ABI
@@ -346,6 +362,43 @@ int trellis_decode_tiles(const trellis_desc* W, uint32_t tile_begin, uint32_t nt
     case 2: return launch_decode_k<2>(W->codebook, W->V, W->bits, tile_begin, ntiles, out, st);
     case 3: return launch_decode_k<3>(W->codebook, W->V, W->bits, tile_begin, ntiles, out, st);
     default: return launch_decode_k<4>(W->codebook, W->V, W->bits, tile_begin, ntiles, out, st);
+  }
+}
+
+int trellis_embed_rows(const trellis_desc* W, const int32_t* tokens, int ntok, void* out,
+                       int64_t ldo, int out_dtype, void* stream) {
+  const int v = validate(W);
+  if (v) return v;
+  if (ntok < 0) return TRELLIS_ERR_BATCH;
+  if (ntok == 0) return TRELLIS_OK;
+  if (!tokens || !out) return TRELLIS_ERR_NULL;
+  if (out_dtype != TRELLIS_F32 && out_dtype != TRELLIS_F16) return TRELLIS_ERR_DTYPE;
+  if (ntok > 1 && ldo < W->k_in) return TRELLIS_ERR_ALIGN;
+  EmbedArgs a;
+  a.bits = W->bits;
+  a.su = W->su;
+  a.sv = W->sv;
+  a.isc = W->isc_scaled;
+  a.osc = W->osc;
+  a.tokens = tokens;
+  a.out = out;
+  a.ldo = ntok > 1 ? ldo : W->k_in;
+  a.n = W->n_out;
+  a.k = W->k_in;
+  a.tiles_in = W->k_in / 16;
+  a.block_in = W->block_in;
+  a.block_out = W->block_out;
+  a.nblk = W->k_in / W->block_in;
+  a.nrm = (1.0f / std::sqrt(static_cast<float>(W->block_in))) *
+          (1.0f / std::sqrt(static_cast<float>(W->block_out)));
+  a.out_f16 = out_dtype == TRELLIS_F16;
+  const uint64_t grid = static_cast<uint64_t>(ntok) * a.nblk;
+  if (grid > 0x7FFFFFFFull) return TRELLIS_ERR_BATCH;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (W->K) {
+    case 2: return launch_embed_k<2>(W->codebook, W->V, a, static_cast<unsigned>(grid), st);
+    case 3: return launch_embed_k<3>(W->codebook, W->V, a, static_cast<unsigned>(grid), st);
+    default: return launch_embed_k<4>(W->codebook, W->V, a, static_cast<unsigned>(grid), st);
   }
 }
 

@@ -136,6 +136,30 @@ class PackedLinear:
         return out
 
 
+    def embed_rows(self, tokens, out: torch.Tensor | None = None,
+                   out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+        """Rows of W_hat with the full restore: out[t] = W_hat[tokens[t]] ([ntok, k_in]);
+        the embedding lookup of a quantized embedding matrix (PackedOps.embedRow,
+        web/packed.js:137-146) for many tokens per call. An id outside [0, n_out) gives
+        a row of zeros."""
+        lib = _capi.load()
+        tok = torch.as_tensor(tokens, dtype=torch.int32, device=self.device).reshape(-1)
+        tok = tok.contiguous()
+        nt = tok.numel()
+        if out is None:
+            out = torch.empty((nt, self.k_in), dtype=out_dtype, device=self.device)
+        if out.dim() != 2 or out.shape != (nt, self.k_in) or out.stride(1) != 1:
+            raise ValueError(f"out must be [{nt}, {self.k_in}] with unit column stride")
+        if out.dtype not in (torch.float16, torch.float32):
+            raise ValueError(f"out dtype {out.dtype} not supported")
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        _capi.check(lib.trellis_embed_rows(
+            ctypes.byref(self.desc), _ptr(tok), nt, _ptr(out), out.stride(0),
+            _capi.DT_F16 if out.dtype == torch.float16 else _capi.DT_F32,
+            ctypes.c_void_p(stream)))
+        return out
+
+
 class PackedGroup:
     """Several packed linears evaluated in ONE launch (trellis_packed_linear_group): e.g.
     q/k/v or gate/up of a decoder block, which the reference dispatches one by one
@@ -218,6 +242,12 @@ class PackedOps:
 
     def linear(self, W: PackedLinear, x: torch.Tensor, out_dtype=torch.float32) -> dict:
         return {"y": W.forward(x, out_dtype=out_dtype), "scale": W.scale}
+
+    def embed_row(self, W: PackedLinear, token_id: int) -> torch.Tensor:
+        """x[H] = W_hat[token_id] (PackedOps.embedRow, web/packed.js:137-146)."""
+        return W.embed_rows([int(token_id)])[0]
+
+    embedRow = embed_row
 
 
 def load_packed(model_dir: str, device="cuda"):
