@@ -208,6 +208,52 @@ def cpu_baseline(budget_s: float = 20.0):
             "ms_per_layer": round(med * 1e3, 2)}
 
 
+def extras(te, torch, dev, steps, K=4):
+    """Next-row measurements on a Qwen3-8B vocab matrix (151936 x 4096, K=4, as the 8B export
+    quantizes the LM head): the batch-1 LM-head GEMV, and embedding-row lookups
+    (trellis_embed_rows) of 1 and 512 random token ids; 4 weight copies (1.2 GB) rotated."""
+    n, k = 151936, 4096
+    copies = 4
+    mats = [make_layers(te, torch, dev, [("lm_head", n, k)], K, 1, seed=100 + c)["lm_head"]
+            for c in range(copies)]
+    x = torch.randn(k, device=dev, dtype=torch.float16)
+    y = torch.empty(n, device=dev, dtype=torch.float32)
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    toks = {nt: torch.randint(0, n, (copies, nt), generator=g, device=dev, dtype=torch.int32)
+            for nt in (1, 512)}
+    outs = {nt: torch.empty((nt, k), device=dev, dtype=torch.float32) for nt in (1, 512)}
+
+    def timed(fn):
+        for c in range(copies):
+            fn(c)
+        torch.cuda.synchronize()
+        gr = capture(torch, lambda: [fn(c) for c in range(copies)])
+        gr.replay()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        reps = max(2, steps // copies)
+        e0.record()
+        for _ in range(reps):
+            gr.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / (reps * copies)
+
+    us_head = timed(lambda c: mats[c].forward(x, out=y))
+    us_emb = {nt: timed(lambda c, nt=nt: mats[c].embed_rows(toks[nt][c], out=outs[nt]))
+              for nt in (1, 512)}
+    del mats
+    torch.cuda.empty_cache()
+    pb = n * k * K // 8
+    return {"matrix": f"{n}x{k} K={K} MCG (Qwen3-8B vocab)",
+            "lm_head_b1_us": round(us_head, 2),
+            "lm_head_b1_GBps": round(pb / (us_head * 1e-6) / 1e9, 1),
+            "embed_rows_1_us": round(us_emb[1], 2),
+            "embed_rows_512_us": round(us_emb[512], 2),
+            "embed_rows_512_tokens_per_s": round(512 / (us_emb[512] * 1e-6), 0)}
+
+
 def block_flops(layers, B):
     return sum(2 * B * n * k for _, n, k in layers)
 
@@ -223,6 +269,8 @@ def main():
     ap.add_argument("--no-batch64", action="store_true", help="skip the batch-64 MFMA figure")
     ap.add_argument("--sweep", action="store_true", help="add BASELINE configs[4] (K x V sweep)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the LM-head GEMV and embedding-row lookup figures")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     args = ap.parse_args()
 
@@ -290,6 +338,12 @@ def main():
                                   "pct_of_hbm_peak": round(100 * pb / ssec / 1e9 / HBM_PEAK_GBS, 2),
                                   "tflops": round(fl / ssec / 1e12, 2)})
 
+    extra = None
+    if not args.no_extras and B == 1:
+        log("[bench] extras: LM head (K=4) and embedding rows")
+        extra = extras(te, torch, dev, max(40, args.steps // 5))
+        log(f"[bench] extras {extra}")
+
     # known-size copy for the HBM-counter scale factor (FETCH_SIZE / WRITE_SIZE)
     src = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
@@ -321,7 +375,8 @@ def main():
                    "us_per_group_launch": us_group,
                    "us_per_layer_single_launch": us_layer,
                    "batch64": batch64,
-                   "sweep_configs4": sweep},
+                   "sweep_configs4": sweep,
+                   "next_rows": extra},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_from_profile() if B == 1 and K == 3 and V == 1 else None,
