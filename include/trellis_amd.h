@@ -127,6 +127,22 @@ int trellis_decode_tiles(const trellis_desc *W, uint32_t tile_begin, uint32_t nt
 int trellis_embed_rows(const trellis_desc *W, const int32_t *tokens, int ntok, void *out,
                        int64_t ldo, int out_dtype, void *stream);
 
+/* Tail-biting trellis encode of z-space tiles (the encoder side of the format): the
+ * counterpart of the reference's Triton encoder viterbi_tb_triton and of qtip.viterbi_tb
+ * (src/trellis/viterbi_triton.py:34-129, src/trellis/qtip.py:124-196; L = 16, T = 256,
+ * V = 1, QTIP's two-pass tail-biting). For each tile, the minimum squared-error path of
+ * the K-bit bitshift trellis under `codebook`:
+ *   w:    device f32 [ntiles][256] targets in tile order t = (row%16)*16 + col%16
+ *   bits: device u32 [ntiles][8K] packed symbols in the reference's reversed stream
+ *         layout (scripts/export_packed.py:27-35), ready for trellis_desc.bits
+ *   dq:   device f32 [ntiles][256] codebook values of the chosen states, or NULL
+ * The DP is exact (every state of every step; ties keep the smallest candidate and the
+ * smallest final edge). The workspace (trellis_encode_workspace_bytes, 256-byte aligned)
+ * holds the backpointers of the tiles in flight; it needs no initialisation. */
+int trellis_encode_workspace_bytes(int K, uint32_t ntiles, size_t *bytes);
+int trellis_encode_tiles(const float *w, uint32_t ntiles, int K, int codebook, uint32_t *bits,
+                         float *dq, void *workspace, size_t ws_bytes, void *stream);
+
 /* Human-readable name of a status code. */
 const char *trellis_strerror(int status);
 

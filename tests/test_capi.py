@@ -81,6 +81,20 @@ def test_embed_rows_rejects_before_launch(te):
     assert lib.trellis_embed_rows(ctypes.byref(d), 16, 2, 16, 255, 0, None) == 8
 
 
+def test_encode_tiles_rejects_before_launch(te):
+    """trellis_encode_tiles validates K, codebook, pointers and workspace on the host."""
+    lib = te.library()
+    n = ctypes.c_size_t(0)
+    assert lib.trellis_encode_workspace_bytes(5, 10, ctypes.byref(n)) == 4
+    assert lib.trellis_encode_workspace_bytes(3, 10, None) == 1
+    assert lib.trellis_encode_tiles(16, 10, 1, 0, 16, None, 256, 1 << 30, None) == 4
+    assert lib.trellis_encode_tiles(16, 10, 3, 7, 16, None, 256, 1 << 30, None) == 6
+    assert lib.trellis_encode_tiles(None, 10, 3, 0, 16, None, 256, 1 << 30, None) == 1
+    assert lib.trellis_encode_tiles(16, 0, 3, 0, None, None, None, 0, None) == 0
+    assert lib.trellis_encode_tiles(16, 10, 3, 0, 16, None, None, 0, None) == 10
+    assert lib.trellis_encode_tiles(16, 10, 3, 0, 16, None, 256 + 8, 1 << 30, None) == 8
+
+
 def test_workspace_plan_is_bounded(te):
     """Workspace for the largest BASELINE shape stays small (partials of 128-row blocks)."""
     lib = te.library()

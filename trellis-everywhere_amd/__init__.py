@@ -13,7 +13,7 @@ from .format import PackedRecord, fit_block, read_packed, write_packed
 
 __all__ = ["PackedRecord", "read_packed", "write_packed", "fit_block", "TrellisError",
            "TrellisLibraryMissing", "PackedLinear", "PackedGroup", "PackedOps", "load_packed",
-           "library"]
+           "encode_tiles", "library"]
 
 
 def library():
@@ -23,7 +23,7 @@ def library():
 
 def __getattr__(name):
     # torch-dependent pieces load lazily so the format tools import without torch
-    if name in ("PackedLinear", "PackedGroup", "PackedOps", "load_packed"):
+    if name in ("PackedLinear", "PackedGroup", "PackedOps", "load_packed", "encode_tiles"):
         from . import packed_linear
         return getattr(packed_linear, name)
     raise AttributeError(name)

@@ -28,7 +28,8 @@ STATUS_NAMES = {
 # every symbol include/trellis_amd.h declares
 EXPORTED = ("trellis_workspace_bytes", "trellis_packed_linear", "trellis_decode_tiles",
             "trellis_strerror", "trellis_version", "trellis_workspace_bytes_group",
-            "trellis_packed_linear_group", "trellis_embed_rows")
+            "trellis_packed_linear_group", "trellis_embed_rows",
+            "trellis_encode_workspace_bytes", "trellis_encode_tiles")
 
 
 class TrellisLibraryMissing(RuntimeError):
@@ -97,6 +98,13 @@ def load(path: str | None = None):
     lib.trellis_embed_rows.argtypes = [D, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
                                        ctypes.c_int64, ctypes.c_int, ctypes.c_void_p]
     lib.trellis_embed_rows.restype = ctypes.c_int
+    lib.trellis_encode_workspace_bytes.argtypes = [ctypes.c_int, ctypes.c_uint32,
+                                                   ctypes.POINTER(ctypes.c_size_t)]
+    lib.trellis_encode_workspace_bytes.restype = ctypes.c_int
+    lib.trellis_encode_tiles.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_int,
+                                         ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                         ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    lib.trellis_encode_tiles.restype = ctypes.c_int
     lib.trellis_strerror.argtypes = [ctypes.c_int]
     lib.trellis_strerror.restype = ctypes.c_char_p
     lib.trellis_version.argtypes = []

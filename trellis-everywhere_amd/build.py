@@ -14,7 +14,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libtrellis_amd.so")
 SOURCES = ["trellis_amd.hip", "kernels_k2.hip", "kernels_k3.hip", "kernels_k4.hip"]
-HEADERS = ["decode.h", "common.h", "gemv.h", "bgemm.h", "launch.h", "embed.h"]
+HEADERS = ["decode.h", "common.h", "gemv.h", "bgemm.h", "launch.h", "embed.h", "encode.h"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"

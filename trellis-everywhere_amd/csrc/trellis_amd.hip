@@ -14,6 +14,7 @@
 #define TRELLIS_BFOLD_DEFINE
 #include "launch.h"
 #include "embed.h"
+#include "encode.h"
 
 using namespace trellis;
 
@@ -300,6 +301,22 @@ int launch_embed_k(int cb, int V, const EmbedArgs& a, unsigned grid, hipStream_t
   return V == 2 ? launch_embed_kv<K, 2>(cb, a, grid, st) : launch_embed_kv<K, 1>(cb, a, grid, st);
 }
 
+// Viterbi encoder: one workgroup per CU, persistent over the tiles.
+unsigned encode_grid(uint32_t ntiles) {
+  const unsigned cus = static_cast<unsigned>(device_cus());
+  return ntiles < cus ? ntiles : cus;
+}
+
+template <int K>
+int launch_encode_k(int cb, const VitArgs& a, unsigned grid, hipStream_t st) {
+  switch (cb) {
+    case CB_MCG: hipLaunchKernelGGL((viterbi_kernel<K, CB_MCG>), dim3(grid), dim3(VIT_THREADS), 0, st, a); break;
+    case CB_3INST: hipLaunchKernelGGL((viterbi_kernel<K, CB_3INST>), dim3(grid), dim3(VIT_THREADS), 0, st, a); break;
+    default: hipLaunchKernelGGL((viterbi_kernel<K, CB_1MAD>), dim3(grid), dim3(VIT_THREADS), 0, st, a); break;
+  }
+  return hipGetLastError() == hipSuccess ? TRELLIS_OK : TRELLIS_ERR_LAUNCH;
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------- C ABI
@@ -399,6 +416,37 @@ int trellis_embed_rows(const trellis_desc* W, const int32_t* tokens, int ntok, v
     case 2: return launch_embed_k<2>(W->codebook, W->V, a, static_cast<unsigned>(grid), st);
     case 3: return launch_embed_k<3>(W->codebook, W->V, a, static_cast<unsigned>(grid), st);
     default: return launch_embed_k<4>(W->codebook, W->V, a, static_cast<unsigned>(grid), st);
+  }
+}
+
+int trellis_encode_workspace_bytes(int K, uint32_t ntiles, size_t* bytes) {
+  if (!bytes) return TRELLIS_ERR_NULL;
+  if (K < 2 || K > 4) return TRELLIS_ERR_K;
+  *bytes = static_cast<size_t>(encode_grid(ntiles)) * vit_bp_bytes(K);
+  return TRELLIS_OK;
+}
+
+int trellis_encode_tiles(const float* w, uint32_t ntiles, int K, int codebook, uint32_t* bits,
+                         float* dq, void* workspace, size_t ws_bytes, void* stream) {
+  if (K < 2 || K > 4) return TRELLIS_ERR_K;
+  if (codebook < TRELLIS_CB_MCG || codebook > TRELLIS_CB_1MAD) return TRELLIS_ERR_CODEBOOK;
+  if (ntiles == 0) return TRELLIS_OK;
+  if (!w || !bits) return TRELLIS_ERR_NULL;
+  const unsigned grid = encode_grid(ntiles);
+  if (!workspace || ws_bytes < static_cast<size_t>(grid) * vit_bp_bytes(K))
+    return TRELLIS_ERR_WORKSPACE;
+  if (reinterpret_cast<uintptr_t>(workspace) % 256) return TRELLIS_ERR_ALIGN;
+  VitArgs a;
+  a.w = w;
+  a.bits = bits;
+  a.dq = dq;
+  a.bp = static_cast<uint32_t*>(workspace);
+  a.ntiles = ntiles;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (K) {
+    case 2: return launch_encode_k<2>(codebook, a, grid, st);
+    case 3: return launch_encode_k<3>(codebook, a, grid, st);
+    default: return launch_encode_k<4>(codebook, a, grid, st);
   }
 }
 

@@ -250,6 +250,30 @@ class PackedOps:
     embedRow = embed_row
 
 
+def encode_tiles(w: torch.Tensor, K: int, codebook: str = "mcg", want_dq: bool = True):
+    """Tail-biting trellis encode of z-space tiles on the GPU (trellis_encode_tiles; the
+    reference's viterbi_tb_triton / qtip.viterbi_tb, src/trellis/viterbi_triton.py:110-129).
+    w: [ntiles, 256] float32 targets in tile order (row%16)*16 + col%16, on the GPU.
+    Returns (bits int32 [ntiles, 8K] in the packed format, dq [ntiles, 256] or None)."""
+    lib = _capi.load()
+    if w.dim() != 2 or w.shape[1] != 256:
+        raise ValueError("w must be [ntiles, 256]")
+    w = w.to(torch.float32).contiguous()
+    nt = w.shape[0]
+    if codebook not in _capi.CB_IDS:
+        raise ValueError(f"unknown codebook {codebook!r}")
+    bits = torch.empty((nt, 8 * K), dtype=torch.int32, device=w.device)
+    dq = torch.empty((nt, 256), dtype=torch.float32, device=w.device) if want_dq else None
+    nbytes = ctypes.c_size_t(0)
+    _capi.check(lib.trellis_encode_workspace_bytes(int(K), nt, ctypes.byref(nbytes)))
+    ws = torch.empty(max(int(nbytes.value), 256), dtype=torch.uint8, device=w.device)
+    stream = torch.cuda.current_stream(w.device).cuda_stream
+    _capi.check(lib.trellis_encode_tiles(_ptr(w), nt, int(K), _capi.CB_IDS[codebook], _ptr(bits),
+                                         _ptr(dq) if want_dq else None, _ptr(ws), ws.numel(),
+                                         ctypes.c_void_p(stream)))
+    return bits, dq
+
+
 def load_packed(model_dir: str, device="cuda"):
     """Mirror of loadPacked / loadPackedSharded (web/packed.js:14-114): returns
     {"cfg": config, "tensors": {name: PackedLinear | torch.Tensor}}."""
