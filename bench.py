@@ -200,12 +200,24 @@ def cpu_baseline(budget_s: float = 20.0):
         mm.append(time.perf_counter() - t0)
     med = statistics.median(times)
     packed = n * k * 3 // 8
+    # the encoder row: the C restatement of the tail-biting Viterbi (oracle/viterbi.c,
+    # OpenMP over tiles) on 4 tiles per core, K=3 MCG
+    from oracle import viterbi as ov
+    wt = np.random.default_rng(1).standard_normal((4 * cores, 256)).astype(np.float32)
+    lut_np = tn.codebook_lut("mcg")
+    ov.viterbi_tb(wt[:cores], 3, lut_np)      # warm-up
+    t0 = time.perf_counter()
+    ov.viterbi_tb(wt, 3, lut_np)
+    enc_s = time.perf_counter() - t0
     return {"value": round(packed / med / 1e9, 4), "unit": "GB/s", "cores": cores,
             "kind": "port",
             "sample": f"Qwen3-8B q_proj 4096x4096 K=3 MCG, torch-CPU decode+restore+matmul "
                       f"(oracle/torch_cpu.py), median of {len(times)} runs = {med * 1e3:.1f} ms; "
                       f"matmul alone on cached W_hat {statistics.median(mm) * 1e3:.2f} ms",
-            "ms_per_layer": round(med * 1e3, 2)}
+            "ms_per_layer": round(med * 1e3, 2),
+            "encode_tiles_per_s": round(wt.shape[0] / enc_s, 1),
+            "encode_sample": f"oracle/viterbi.c tail-biting encode, K=3 MCG, {wt.shape[0]} tiles "
+                             f"on {cores} threads: {enc_s:.2f} s"}
 
 
 def extras(te, torch, dev, steps, K=4):
@@ -241,6 +253,14 @@ def extras(te, torch, dev, steps, K=4):
         return e0.elapsed_time(e1) * 1e3 / (reps * copies)
 
     us_head = timed(lambda c: mats[c].forward(x, out=y))
+    # the encoder row: trellis_encode_tiles on 4096 tiles (16 per workgroup), K=3 MCG
+    wt = torch.randn((4096, 256), device=dev)
+    te.encode_tiles(wt[:256], 3, "mcg", want_dq=False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    te.encode_tiles(wt, 3, "mcg", want_dq=False)
+    torch.cuda.synchronize()
+    enc_s = time.perf_counter() - t0
     us_emb = {nt: timed(lambda c, nt=nt: mats[c].embed_rows(toks[nt][c], out=outs[nt]))
               for nt in (1, 512)}
     del mats
@@ -251,7 +271,9 @@ def extras(te, torch, dev, steps, K=4):
             "lm_head_b1_GBps": round(pb / (us_head * 1e-6) / 1e9, 1),
             "embed_rows_1_us": round(us_emb[1], 2),
             "embed_rows_512_us": round(us_emb[512], 2),
-            "embed_rows_512_tokens_per_s": round(512 / (us_emb[512] * 1e-6), 0)}
+            "embed_rows_512_tokens_per_s": round(512 / (us_emb[512] * 1e-6), 0),
+            "encode_tiles_per_s_K3": round(4096 / enc_s, 1),
+            "encode_8b_block_s_K3": round(753664 / (4096 / enc_s), 2)}
 
 
 def block_flops(layers, B):
