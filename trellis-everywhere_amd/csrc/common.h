@@ -158,32 +158,51 @@ __device__ __forceinline__ int locate_mat(const LinArgs& g, int it, bool by_chun
 }
 
 // ---------------------------------------------------------------- x fold
-// One wave per (matrix, batch row, 128-column chunk): xf = Hb_k(isc * su * x) scaled by
-// 1/sqrt(block_in), stored as (x,x) fp16 pairs. Defined in one translation unit only.
+// xf = Hb_k(isc * su * x) scaled by 1/sqrt(block_in), stored as (x,x) fp16 pairs. One
+// wave per (matrix, 4 batch rows, 128-column chunk): su * isc of the chunk is loaded once
+// for the 4 rows, every load is a range-checked buffer load issued up front (rows past the
+// call's read zeros), and the four transforms run back to back. Defined in one
+// translation unit only.
+constexpr int XFOLD_ROWS = 4;
 #ifdef TRELLIS_XFOLD_DEFINE
 __global__ __launch_bounds__(256) void xfold_kernel(LinArgs g) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int job = blockIdx.x * 4 + wave;
   if (job >= g.total) return;
   const int mi = locate_mat(g, job, true);
   const LinMat& m = g.m[mi];
   const int local = job - m.chunk0;
   const int nch = (m.k + 127) / 128;
-  const int b = local / nch, ch = local % nch;
+  const int rg = local / nch, ch = local % nch;
+  const int b0 = rg * XFOLD_ROWS;
   const int kvalid = min(128, m.k - ch * 128);
-  const int e0 = lane, e1 = lane + 64;
-  const int c0i = ch * 128 + min(e0, kvalid - 1), c1i = ch * 128 + min(e1, kvalid - 1);
-  const long long x0i = b * m.ldx + c0i, x1i = b * m.ldx + c1i;
-  const uint32_t w0 = load_act_word(m.x, x0i, g.x_f16);
-  const uint32_t w1 = load_act_word(m.x, x1i, g.x_f16);
-  const float s0 = m.su[c0i] * m.isc[c0i], s1 = m.su[c1i] * m.isc[c1i];
-  float lo = e0 < kvalid ? act_value(w0, x0i, g.x_f16) * s0 : 0.0f;
-  float hi = e1 < kvalid ? act_value(w1, x1i, g.x_f16) * s1 : 0.0f;
-  fwht_chunk(lo, hi, m.block_in, lane);
+  const int xsh = g.x_f16 ? 1 : 2;
+  const rsrc_t r_x = make_rsrc(m.x, static_cast<unsigned>(g.batch) * static_cast<unsigned>(m.ldx) << xsh);
+  const rsrc_t r_su = make_rsrc(m.su, m.k * 4), r_isc = make_rsrc(m.isc, m.k * 4);
+  const int e0 = ch * 128 + lane, e1 = e0 + 64;
+  const float s0 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r_su, e0 * 4, 0, 0)) *
+                   __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r_isc, e0 * 4, 0, 0));
+  const float s1 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r_su, e1 * 4, 0, 0)) *
+                   __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r_isc, e1 * 4, 0, 0));
+  uint32_t w0[XFOLD_ROWS], w1[XFOLD_ROWS];
+#pragma unroll
+  for (int r = 0; r < XFOLD_ROWS; ++r) {
+    const unsigned row = static_cast<unsigned>((b0 + r) * m.ldx);
+    w0[r] = __builtin_amdgcn_raw_buffer_load_b32(r_x, static_cast<int>(((row + e0) << xsh) & ~3u), 0, 0);
+    w1[r] = __builtin_amdgcn_raw_buffer_load_b32(r_x, static_cast<int>(((row + e1) << xsh) & ~3u), 0, 0);
+  }
   const float nrm = m.nrm_in;
-  uint32_t* dst = m.xf + static_cast<size_t>(b) * m.k + ch * 128;
-  if (e0 < kvalid) dst[e0] = dup_half(lo * nrm);
-  if (e1 < kvalid) dst[e1] = dup_half(hi * nrm);
+#pragma unroll
+  for (int r = 0; r < XFOLD_ROWS; ++r) {
+    if (b0 + r >= g.batch) break;
+    // an f16 row stride is even, so the element's half within its word follows e
+    float lo = lane < kvalid ? act_value(w0[r], e0, g.x_f16) * s0 : 0.0f;
+    float hi = lane + 64 < kvalid ? act_value(w1[r], e1, g.x_f16) * s1 : 0.0f;
+    fwht_chunk(lo, hi, m.block_in, lane);
+    uint32_t* dst = m.xf + static_cast<size_t>(b0 + r) * m.k + ch * 128;
+    if (lane < kvalid) dst[lane] = dup_half(lo * nrm);
+    if (lane + 64 < kvalid) dst[lane + 64] = dup_half(hi * nrm);
+  }
 }
 #endif
 

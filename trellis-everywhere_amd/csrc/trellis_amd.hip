@@ -531,7 +531,7 @@ int trellis_packed_linear_group(const trellis_desc* const* W, int count, const v
       g.m[i].x = static_cast<const char*>(x[i]) + static_cast<size_t>(b0) * ldx[i] * xes;
       g.m[i].y = static_cast<char*>(y[i]) + static_cast<size_t>(b0) * ldy[i] * yes;
       g.m[i].chunk0 = chunk0;
-      chunk0 += g.batch * ((W[i]->k_in + 127) / 128);
+      chunk0 += ((g.batch + XFOLD_ROWS - 1) / XFOLD_ROWS) * ((W[i]->k_in + 127) / 128);
     }
     v = p.gemv ? launch_gemv(W[0]->K, W[0]->codebook, W[0]->V, p.kc, g, st)
                : launch_bgemm(W[0]->K, W[0]->codebook, W[0]->V, p.nc, g, chunk0, nfold, st);
