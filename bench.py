@@ -104,7 +104,7 @@ def capture(torch, fn):
 
 
 def run_block(te, torch, dev, layers, groups, B, K, V, steps, warmup, min_bytes=1.0e9,
-              per_launch=True):
+              per_launch=True, mma_f16=False):
     """Time `steps` replays of the block (its launches in order) over distinct weight copies.
     Returns (seconds per step, {group: us per launch}, {layer: us per launch})."""
     block_bytes = sum(n * k * K // 8 for _, n, k in layers)
@@ -122,10 +122,10 @@ def run_block(te, torch, dev, layers, groups, B, K, V, steps, warmup, min_bytes=
     def step(c, only=None):
         for gname, grp, members in grps[c % copies]:
             if only is None or gname == only:
-                grp.forward([xs[m] for m in members], [ys[m] for m in members])
+                grp.forward([xs[m] for m in members], [ys[m] for m in members], mma_f16=mma_f16)
 
     def single(c, name):
-        blocks[c % copies][name].forward(xs[name], out=ys[name])
+        blocks[c % copies][name].forward(xs[name], out=ys[name], mma_f16=mma_f16)
 
     for c in range(copies):            # allocates every workspace once, before capture
         step(c)
@@ -289,6 +289,8 @@ def main():
     ap.add_argument("--K", type=int, default=3)
     ap.add_argument("--V", type=int, default=1)
     ap.add_argument("--no-batch64", action="store_true", help="skip the batch-64 MFMA figure")
+    ap.add_argument("--mma-f16", action="store_true",
+                    help="batch >= 2: the fp16-weight MFMA mode (TRELLIS_MMA_F16) for the block run")
     ap.add_argument("--sweep", action="store_true", help="add BASELINE configs[4] (K x V sweep)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
@@ -310,7 +312,7 @@ def main():
 
     log(f"[bench] block batch {B} K={K} V={V}")
     sec, us_group, us_layer, copies = run_block(te, torch, dev, LAYERS, GROUPS, B, K, V,
-                                                args.steps, args.warmup)
+                                                args.steps, args.warmup, mma_f16=args.mma_f16)
     gbs = block_bytes / sec / 1e9
     dom_us = us_group[DOMINANT]
     dom_bytes = 2 * 12288 * 4096 * K // 8
@@ -338,6 +340,19 @@ def main():
                                 "avg_launch_us": g64[DOMINANT],
                                 "algorithmic_flops_per_launch": dom_fl}}
         log(f"[bench] batch 64: {batch64['us_per_block']} us/block, {batch64['tflops']} TFLOP/s")
+        # the same block with the fp16-weight MFMA mode (each codebook value rounded once
+        # to fp16, one MAC per weight; max rel err ~2-3e-4 against the exact default)
+        s64h, g64h, _, _ = run_block(te, torch, dev, LAYERS, GROUPS, 64, K, V,
+                                     max(20, args.steps // 10), max(3, args.warmup // 5),
+                                     per_launch=True, mma_f16=True)
+        dom_tfh = dom_fl / (g64h[DOMINANT] * 1e-6) / 1e12
+        batch64["mma_f16"] = {"us_per_block": round(s64h * 1e6, 2),
+                              "tflops": round(fl / s64h / 1e12, 2),
+                              "mfma_frac_of_fp16_peak": round(fl / s64h / 1e12 / MFMA_FP16_PEAK_TFLOPS, 4),
+                              "us_per_group_launch": g64h,
+                              "gate_up_tflops": round(dom_tfh, 2)}
+        log(f"[bench] batch 64 mma_f16: {batch64['mma_f16']['us_per_block']} us/block, "
+            f"{batch64['mma_f16']['tflops']} TFLOP/s")
 
     sweep = None
     if args.sweep:
@@ -389,6 +404,7 @@ def main():
         "config": {"workload": f"Qwen3-8B decoder-block linears (q,k,v,o,gate,up,down), K={K}, "
                                f"MCG, V={V}, batch {B}",
                    "batch": B, "K": K, "V": V, "codebook": "mcg",
+                   "mma_f16": bool(args.mma_f16 and B > 1),
                    "block_packed_bytes": block_bytes, "weight_copies": copies,
                    "rotated_bytes": block_bytes * copies,
                    "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),

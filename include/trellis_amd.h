@@ -54,8 +54,21 @@ typedef enum trellis_status {
   TRELLIS_ERR_BATCH = 11,      /* batch < 1 */
   TRELLIS_ERR_RANGE = 12,      /* tile range outside the matrix */
   TRELLIS_ERR_LAUNCH = 13,     /* the HIP runtime rejected a launch */
-  TRELLIS_ERR_GROUP = 14       /* group of 0 or more than 8 linears, or mixed K / V / codebook */
+  TRELLIS_ERR_GROUP = 14,      /* group of 0 or more than 8 linears, or mixed K / V / codebook */
+  TRELLIS_ERR_FLAGS = 15       /* unknown bits in the flags of an _ex call */
 } trellis_status;
+
+/* Flags of trellis_packed_linear_ex / trellis_packed_linear_group_ex. */
+enum trellis_flags {
+  /* Batch >= 2 only (batch 1 ignores it): round each decoded codebook value once to fp16
+   * (hi + lo in one fp16 add, i.e. the reference's exact fp32 sum, qtip.py:28-29, rounded
+   * to nearest) and multiply it by the fp16 activation once, instead of the exact (hi, lo)
+   * pair against a duplicated activation: half the MFMAs and half the activation bytes of
+   * the batched kernel. Max rel err against the exact path ~2-3e-4 (MCG, 3INST; 1MAD
+   * values are exact fp16 integers either way). The reference's Triton codebook adds the
+   * halves in fp16 the same way (src/trellis/viterbi_triton.py:29-31). */
+  TRELLIS_MMA_F16 = 1
+};
 
 /* One packed trellis linear as the loader record holds it (web/packed.js:53-62,
  * 93-103): device pointers to the packed words and f32 metadata. */
@@ -97,6 +110,13 @@ int trellis_packed_linear(const trellis_desc *W, const void *x, int64_t ldx, int
                           int x_dtype, void *y, int64_t ldy, int y_dtype, void *workspace,
                           size_t ws_bytes, void *stream);
 
+/* trellis_packed_linear with flags (enum trellis_flags; 0 = trellis_packed_linear). No
+ * reference counterpart: the precision choice of the batched MFMAs. The workspace size
+ * from trellis_workspace_bytes covers every flag. */
+int trellis_packed_linear_ex(const trellis_desc *W, const void *x, int64_t ldx, int batch,
+                             int x_dtype, void *y, int64_t ldy, int y_dtype, void *workspace,
+                             size_t ws_bytes, int flags, void *stream);
+
 /* Several independent packed linears in ONE launch (no reference counterpart: the
  * reference dispatches every linear separately, web/model.js:80-100). Intended for the
  * linears of a decoder block that share an input (q/k/v, gate/up) or any set whose
@@ -109,6 +129,11 @@ int trellis_packed_linear_group(const trellis_desc *const *W, int count, const v
                                 const int64_t *ldx, int batch, int x_dtype, void *const *y,
                                 const int64_t *ldy, int y_dtype, void *workspace,
                                 size_t ws_bytes, void *stream);
+/* trellis_packed_linear_group with flags (enum trellis_flags), as trellis_packed_linear_ex. */
+int trellis_packed_linear_group_ex(const trellis_desc *const *W, int count,
+                                   const void *const *x, const int64_t *ldx, int batch,
+                                   int x_dtype, void *const *y, const int64_t *ldy, int y_dtype,
+                                   void *workspace, size_t ws_bytes, int flags, void *stream);
 
 /* Decode z-space tiles [tile_begin, tile_begin+ntiles) to fp32, 256 values per tile in
  * tile order t = (row%16)*16 + col%16. The bit-exact probe of the decode: restates

@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol(te):
 
 def test_strerror_names_every_status(te):
     lib = te.library()
-    for code in range(0, 15):
+    for code in range(0, 16):
         assert lib.trellis_strerror(code).decode() not in ("", "unknown trellis status")
     assert lib.trellis_strerror(99).decode() == "unknown trellis status"
 
@@ -64,6 +64,24 @@ def test_packed_linear_rejects_before_launch(te):
         assert lib.trellis_packed_linear(ctypes.byref(d), 16, 256, 1, 0, 16, 128, 0, None, 0,
                                          None) == 10
     assert lib.trellis_decode_tiles(ctypes.byref(d), 100, 100, 16, None) == 12
+
+
+def test_packed_linear_ex_flags(te):
+    """Unknown flag bits are rejected on the host (TRELLIS_ERR_FLAGS); the workspace size
+    covers every flag."""
+    lib = te.library()
+    d = _desc(te)
+    assert lib.trellis_packed_linear_ex(ctypes.byref(d), 16, 256, 2, 0, 16, 128, 0, None, 0, 2,
+                                        None) == 15
+    assert lib.trellis_packed_linear_ex(ctypes.byref(d), 16, 256, 2, 0, 16, 128, 0, None, 0, 1,
+                                        None) == 10
+    arr = (ctypes.POINTER(te._capi.TrellisDesc) * 1)(ctypes.pointer(d))
+    xp = (ctypes.c_void_p * 1)(16)
+    ld = (ctypes.c_int64 * 1)(256)
+    ldy = (ctypes.c_int64 * 1)(128)
+    assert lib.trellis_packed_linear_group_ex(arr, 1, xp, ld, 2, 0, xp, ldy, 0, None, 0, -1,
+                                              None) == 15
+    assert te._capi.MMA_F16 == 1
 
 
 def test_embed_rows_rejects_before_launch(te):

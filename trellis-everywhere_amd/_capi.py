@@ -22,14 +22,18 @@ STATUS_NAMES = {
     4: "TRELLIS_ERR_K", 5: "TRELLIS_ERR_V", 6: "TRELLIS_ERR_CODEBOOK", 7: "TRELLIS_ERR_NWORDS",
     8: "TRELLIS_ERR_ALIGN", 9: "TRELLIS_ERR_DTYPE", 10: "TRELLIS_ERR_WORKSPACE",
     11: "TRELLIS_ERR_BATCH", 12: "TRELLIS_ERR_RANGE", 13: "TRELLIS_ERR_LAUNCH",
-    14: "TRELLIS_ERR_GROUP",
+    14: "TRELLIS_ERR_GROUP", 15: "TRELLIS_ERR_FLAGS",
 }
+
+# enum trellis_flags
+MMA_F16 = 1
 
 # every symbol include/trellis_amd.h declares
 EXPORTED = ("trellis_workspace_bytes", "trellis_packed_linear", "trellis_decode_tiles",
             "trellis_strerror", "trellis_version", "trellis_workspace_bytes_group",
             "trellis_packed_linear_group", "trellis_embed_rows",
-            "trellis_encode_workspace_bytes", "trellis_encode_tiles")
+            "trellis_encode_workspace_bytes", "trellis_encode_tiles",
+            "trellis_packed_linear_ex", "trellis_packed_linear_group_ex")
 
 
 class TrellisLibraryMissing(RuntimeError):
@@ -83,6 +87,11 @@ def load(path: str | None = None):
                                           ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t,
                                           ctypes.c_void_p]
     lib.trellis_packed_linear.restype = ctypes.c_int
+    lib.trellis_packed_linear_ex.argtypes = [D, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
+                                             ctypes.c_int, ctypes.c_void_p, ctypes.c_int64,
+                                             ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t,
+                                             ctypes.c_int, ctypes.c_void_p]
+    lib.trellis_packed_linear_ex.restype = ctypes.c_int
     PP = ctypes.POINTER(ctypes.c_void_p)
     I64P = ctypes.POINTER(ctypes.c_int64)
     lib.trellis_workspace_bytes_group.argtypes = [ctypes.POINTER(D), ctypes.c_int, ctypes.c_int,
@@ -92,6 +101,11 @@ def load(path: str | None = None):
                                                 ctypes.c_int, ctypes.c_int, PP, I64P, ctypes.c_int,
                                                 ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
     lib.trellis_packed_linear_group.restype = ctypes.c_int
+    lib.trellis_packed_linear_group_ex.argtypes = [ctypes.POINTER(D), ctypes.c_int, PP, I64P,
+                                                   ctypes.c_int, ctypes.c_int, PP, I64P,
+                                                   ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t,
+                                                   ctypes.c_int, ctypes.c_void_p]
+    lib.trellis_packed_linear_group_ex.restype = ctypes.c_int
     lib.trellis_decode_tiles.argtypes = [D, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p,
                                          ctypes.c_void_p]
     lib.trellis_decode_tiles.restype = ctypes.c_int

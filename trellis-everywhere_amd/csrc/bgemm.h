@@ -75,19 +75,23 @@ __device__ __forceinline__ void bg_out_fold(const LinArgs& g, const LinMat& m, c
   }
 }
 
-// k-step: 8 tile columns for up to 64 batch columns, 4 for 128 (LDS holds two B steps)
-template <int NC> struct BgStep { static constexpr int KT = NC <= 4 ? 8 : 4; };
+// k-step: 8 tile columns for up to 64 batch columns, 4 for 128 (LDS holds two B steps);
+// always 8 in the fp16-weight mode, whose B words are half as many per column
+template <int NC, int F16> struct BgStep { static constexpr int KT = (F16 || NC <= 4) ? 8 : 4; };
 constexpr int BG_WAVES = 16;
 constexpr int BG_KL = 4;   // k-lanes: waves of one band pair splitting each step's tiles
 
-template <int K, int CB, int V, int NC>
+template <int K, int CB, int V, int NC, int F16>
 __global__ __launch_bounds__(64 * BG_WAVES) void bgemm_kernel(LinArgs g) {
   constexpr int NWK = 8 * K;
-  constexpr int KT = BgStep<NC>::KT;               // tile columns per k-step
-  constexpr int TPL = KT / BG_KL;                  // tiles per band per k-lane per step
-  constexpr int XW = KT * 16 + 8;                  // LDS words per B row (+8: bank spread)
+  constexpr int KT = BgStep<NC, F16>::KT;          // tile columns per k-step
+  // tiles per band per k-lane per step: exact mode, tiles kl, kl + 4, ...; fp16-weight
+  // mode, the tile pair 2kl, 2kl + 1 (one MFMA per pair)
+  constexpr int TPL = F16 ? 2 : KT / BG_KL;
+  constexpr int WPT = F16 ? 8 : 16;                // B words per tile column and batch row
+  constexpr int XW = KT * WPT + 8;                 // LDS words per B row (+8: bank spread)
   constexpr int NB = 16 * NC;                      // batch columns per workgroup
-  constexpr int RCH = KT * 4;                      // 16-byte chunks per B row per step
+  constexpr int RCH = KT * WPT / 4;                // 16-byte chunks per B row per step
   constexpr int XCH = NB * RCH;                    // 16-byte B chunks per step
   constexpr int XLOADS = (XCH + 64 * BG_WAVES - 1) / (64 * BG_WAVES);
   constexpr int XBUF = NB * XW;                    // words per B buffer
@@ -96,6 +100,7 @@ __global__ __launch_bounds__(64 * BG_WAVES) void bgemm_kernel(LinArgs g) {
   constexpr int BLOADS = (BCH + 63) / 64;
   constexpr int BSW = BLOADS * 256;                // words per wave buffer: every lane's chunks
   static_assert(NB * 136 <= 2 * XBUF, "epilogue t[NB][136] reuses the B buffers");
+  static_assert(!F16 || KT == 2 * BG_KL, "fp16-weight mode: one tile pair per k-lane per step");
   __shared__ __align__(16) uint32_t xsb[2 * XBUF];
   __shared__ __align__(16) uint32_t bst[BG_WAVES * BSW];
   // epilogue: t[NB][TLS] (rows padded like the B rows, so a fragment's float4 writes
@@ -123,14 +128,14 @@ __global__ __launch_bounds__(64 * BG_WAVES) void bgemm_kernel(LinArgs g) {
 
   // B: rows b0 .. b0 + nbv - 1 of xf (a batch row past the call's reads zeros; columns
   // past the k-range feed only tiles that are not decoded)
-  const rsrc_t r_x = make_rsrc(m.xf + static_cast<size_t>(b0) * m.k,
-                               static_cast<unsigned>(nbv) * m.k * 4);
+  const rsrc_t r_x = make_rsrc(m.xf + static_cast<size_t>(b0) * m.xfw,
+                               static_cast<unsigned>(nbv) * m.xfw * 4);
   unsigned xoff[XLOADS];
 #pragma unroll
   for (int q = 0; q < XLOADS; ++q) {
     const int ch = threadIdx.x + 64 * BG_WAVES * q;
     const int n = ch / RCH, off = ch % RCH;        // batch row, 16-byte chunk of its row
-    xoff[q] = ch < XCH ? static_cast<unsigned>((n * m.k + c0 * 16 + off * 4) * 4) : RSRC_OOB;
+    xoff[q] = ch < XCH ? static_cast<unsigned>((n * m.xfw + c0 * WPT + off * 4) * 4) : RSRC_OOB;
   }
   // packed words from the block's first band to the end of the matrix (bands past the
   // matrix read zeros); lane chunk -> (band of the pair, tile of the k-lane, chunk)
@@ -143,13 +148,14 @@ __global__ __launch_bounds__(64 * BG_WAVES) void bgemm_kernel(LinArgs g) {
     const int ch = lane + 64 * q;
     const int bb = ch / (TPL * CPT), rem = ch % (TPL * CPT);
     const int t = rem / CPT, c = rem % CPT;
-    boff[q] = ch < BCH ? static_cast<unsigned>(((2 * bp + bb) * m.tiles_in + c0 + kl + BG_KL * t) * NWK * 4 + c * 16)
+    const int tile = c0 + (F16 ? 2 * kl + t : kl + BG_KL * t);
+    boff[q] = ch < BCH ? static_cast<unsigned>(((2 * bp + bb) * m.tiles_in + tile) * NWK * 4 + c * 16)
                        : RSRC_OOB;
   }
   u32x4_t xr[2][XLOADS], br[2][BLOADS];
   auto load_step = [&](int s, u32x4_t (&xd)[XLOADS], u32x4_t (&bd)[BLOADS]) {
     // a step past the last reads nothing
-    const unsigned sx = s < nsteps ? static_cast<unsigned>(s * KT * 16 * 4) : RSRC_OOB;
+    const unsigned sx = s < nsteps ? static_cast<unsigned>(s * KT * WPT * 4) : RSRC_OOB;
     const unsigned sb = s < nsteps ? static_cast<unsigned>(s * KT * NWK * 4) : RSRC_OOB;
 #pragma unroll
     for (int q = 0; q < XLOADS; ++q)
@@ -195,20 +201,40 @@ __global__ __launch_bounds__(64 * BG_WAVES) void bgemm_kernel(LinArgs g) {
       load_step(st + 2, xr[h], br[h]);
       if (st < nsteps) {
         const uint32_t* xb = xsb + h * XBUF + r * XW + 4 * gq;
-#pragma unroll
-        for (int t = 0; t < TPL; ++t) {
-          const int j = kl + BG_KL * t;            // tile of the step
-          if (st * KT + j < ntl) {
-            const uint32_t* t0 = mystg + t * NWK;
-            const uint32_t* t1 = mystg + (TPL + t) * NWK;
-            const half8_t A0 = decode_a<K, CB, V>(t0[qp.wa], t0[qp.wb], qp.sh);
-            const half8_t A1 = decode_a<K, CB, V>(t1[qp.wa], t1[qp.wb], qp.sh);
+        if constexpr (F16) {
+          // the pair 2kl, 2kl + 1 of the step; past an odd last tile the second tile's
+          // words decode to finite values that meet zero activations (xfold_kernel)
+          if (st * KT + 2 * kl < ntl) {
+            const uint32_t* p0 = mystg;                 // band 2bp: tiles 2kl, 2kl + 1
+            const uint32_t* p1 = mystg + TPL * NWK;     // band 2bp + 1
+            const half8_t A0 = decode_a_pair<K, CB, V>(p0[qp.wa], p0[qp.wb], p0[NWK + qp.wa],
+                                                       p0[NWK + qp.wb], qp.sh);
+            const half8_t A1 = decode_a_pair<K, CB, V>(p1[qp.wa], p1[qp.wb], p1[NWK + qp.wa],
+                                                       p1[NWK + qp.wb], qp.sh);
 #pragma unroll
             for (int c = 0; c < NC; ++c) {
               const half8_t B = __builtin_bit_cast(
-                  half8_t, *reinterpret_cast<const u32x4_t*>(xb + c * 16 * XW + j * 16));
+                  half8_t, *reinterpret_cast<const u32x4_t*>(xb + c * 16 * XW + kl * 16));
               acc[0][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, B, acc[0][c], 0, 0, 0);
               acc[1][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, B, acc[1][c], 0, 0, 0);
+            }
+          }
+        } else {
+#pragma unroll
+          for (int t = 0; t < TPL; ++t) {
+            const int j = kl + BG_KL * t;            // tile of the step
+            if (st * KT + j < ntl) {
+              const uint32_t* t0 = mystg + t * NWK;
+              const uint32_t* t1 = mystg + (TPL + t) * NWK;
+              const half8_t A0 = decode_a<K, CB, V>(t0[qp.wa], t0[qp.wb], qp.sh);
+              const half8_t A1 = decode_a<K, CB, V>(t1[qp.wa], t1[qp.wb], qp.sh);
+#pragma unroll
+              for (int c = 0; c < NC; ++c) {
+                const half8_t B = __builtin_bit_cast(
+                    half8_t, *reinterpret_cast<const u32x4_t*>(xb + c * 16 * XW + j * 16));
+                acc[0][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, B, acc[0][c], 0, 0, 0);
+                acc[1][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, B, acc[1][c], 0, 0, 0);
+              }
             }
           }
         }

@@ -33,11 +33,13 @@ struct LinMat {
   const float* osc;
   const void* x;
   void* y;
-  uint32_t* xf;         // workspace: [batch][k] fp16 (x,x) pairs
+  uint32_t* xf;         // workspace: [batch][xfw words] folded activations (xfold_kernel)
   float* part;          // workspace: split-K partial sums (S > 1)
   unsigned* tickets;    // workspace: [n_ob] arrival counters (batch 1, S > 1), zero between calls
   long long ldx, ldy;
   int n, k, tiles_in, block_in, block_out;
+  int xfw;              // words per xf row: k ((x, x) fp16 pairs), or kp / 2 in the fp16-weight
+                        // mode (kp = k rounded up to 32; fp16 values, tile pairs interleaved)
   float nrm_in, nrm_out;  // 1 / sqrt(block_in), 1 / sqrt(block_out), rounded as fp32 ops
   int n_ob, S;
   unsigned s_inv;       // ceil(2^32 / S) for S > 1 (item / S = umulhi(item, s_inv)), else 0
@@ -54,6 +56,7 @@ struct LinArgs {
   int batch;            // batch rows of the call
   int x_f16, y_f16;
   int kr;               // tile columns per k-range
+  int mma_f16;          // batched path: codebook values rounded to fp16, one MAC per weight
 };
 
 // Range-checked buffer loads: a buffer resource over [base, base + bytes); an offset at or
@@ -157,6 +160,14 @@ __device__ __forceinline__ int locate_mat(const LinArgs& g, int it, bool by_chun
   return mi;
 }
 
+// The fp16-weight mode's B layout: the 32 activations of a tile pair (columns 32p .. 32p+31)
+// are stored as, for g = 0..3, columns 32p + 4g .. +3 then 32p + 16 + 4g .. +3, so the 16
+// bytes at half 32p + 8g hold the k-slots 8g .. 8g+7 that lane group g of an MFMA fragment
+// reads: the first tile's columns 4g .. 4g+3, then the second tile's (decode_a_pair).
+__device__ __forceinline__ int xf_pair_slot(int e) {
+  return (e & ~31) + 8 * ((e >> 2) & 3) + 4 * ((e >> 4) & 1) + (e & 3);
+}
+
 // ---------------------------------------------------------------- x fold
 // xf = Hb_k(isc * su * x) scaled by 1/sqrt(block_in), stored as (x,x) fp16 pairs. One
 // wave per (matrix, 4 batch rows, 128-column chunk): su * isc of the chunk is loaded once
@@ -199,9 +210,18 @@ __global__ __launch_bounds__(256) void xfold_kernel(LinArgs g) {
     float lo = lane < kvalid ? act_value(w0[r], e0, g.x_f16) * s0 : 0.0f;
     float hi = lane + 64 < kvalid ? act_value(w1[r], e1, g.x_f16) * s1 : 0.0f;
     fwht_chunk(lo, hi, m.block_in, lane);
-    uint32_t* dst = m.xf + static_cast<size_t>(b0 + r) * m.k + ch * 128;
-    if (lane < kvalid) dst[lane] = dup_half(lo * nrm);
-    if (lane + 64 < kvalid) dst[lane + 64] = dup_half(hi * nrm);
+    if (g.mma_f16) {
+      // fp16 values in tile-pair order (xf_pair_slot); columns k .. kp - 1 of the last
+      // pair are written as zeros (lo and hi are zero there)
+      _Float16* dst = reinterpret_cast<_Float16*>(m.xf + static_cast<size_t>(b0 + r) * m.xfw);
+      const int kp = 2 * m.xfw;
+      if (e0 < kp) dst[xf_pair_slot(e0)] = static_cast<_Float16>(lo * nrm);
+      if (e1 < kp) dst[xf_pair_slot(e1)] = static_cast<_Float16>(hi * nrm);
+    } else {
+      uint32_t* dst = m.xf + static_cast<size_t>(b0 + r) * m.xfw + ch * 128;
+      if (lane < kvalid) dst[lane] = dup_half(lo * nrm);
+      if (lane + 64 < kvalid) dst[lane + 64] = dup_half(hi * nrm);
+    }
   }
 }
 #endif
@@ -221,6 +241,47 @@ __device__ __forceinline__ half8_t decode_a(uint32_t wlo, uint32_t whi, int sh) 
     }
   }
   return __builtin_bit_cast(half8_t, a4);
+}
+
+// hi + lo of two codebook pairs (hi in the upper half of each word) as one packed pair of
+// fp16 sums: v_add_f16 with SDWA operand selects, one instruction per value. The fp16 add
+// rounds the exact sum of the two halves to nearest even, as a cast of the reference's
+// fp32 sum (qtip.py:28-29, 45, 53) to fp16 does.
+__device__ __forceinline__ uint32_t add_halves2(uint32_t r0, uint32_t r1) {
+  uint32_t d;
+  asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_1 src1_sel:WORD_0\n\t"
+      "v_add_f16_sdwa %0, %2, %2 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_1 src1_sel:WORD_0"
+      : "=&v"(d)
+      : "v"(r0), "v"(r1));
+  return d;
+}
+
+// The A operand of a tile pair in the fp16-weight mode (one MAC per weight): k-slots
+// 8g .. 8g+3 of lane (r, g) hold the first tile's columns 4g .. 4g+3, slots 8g+4 .. 8g+7
+// the second tile's (xf_pair_slot lays B out to match), each codebook value rounded once
+// to fp16. 1MAD's (y - 510) is an exact fp16 integer, as in decode_a.
+template <int K, int CB, int V = 1>
+__device__ __forceinline__ half8_t decode_a_pair(uint32_t wlo0, uint32_t whi0, uint32_t wlo1,
+                                                 uint32_t whi1, int sh) {
+  uint32_t a0[4], a1[4], o[4];
+  decode_quad<K, CB, V>(wlo0, whi0, sh, a0);
+  decode_quad<K, CB, V>(wlo1, whi1, sh, a1);
+  if constexpr (CB == CB_1MAD) {
+    uint32_t h[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int y = static_cast<int>(q < 4 ? a0[q] : a1[q - 4]) - 510;
+      h[q] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(static_cast<float>(y)));
+    }
+#pragma unroll
+    for (int w = 0; w < 4; ++w) o[w] = h[2 * w] | (h[2 * w + 1] << 16);
+  } else {
+    o[0] = add_halves2(a0[0], a0[1]);
+    o[1] = add_halves2(a0[2], a0[3]);
+    o[2] = add_halves2(a1[0], a1[1]);
+    o[3] = add_halves2(a1[2], a1[3]);
+  }
+  return __builtin_bit_cast(half8_t, o);
 }
 
 }  // namespace trellis

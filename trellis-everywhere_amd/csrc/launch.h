@@ -15,7 +15,8 @@ namespace trellis {
 template <int K>
 int launch_gemv_k(int cb, int V, int kc, const LinArgs& g, hipStream_t st);
 
-// bgemm_kernel<K, cb, V, nc> over g.total items (the x fold has been launched before it).
+// bgemm_kernel<K, cb, V, nc, g.mma_f16> over g.total items (the x fold has been launched
+// before it).
 template <int K>
 int launch_bgemm_k(int cb, int V, int nc, const LinArgs& g, hipStream_t st);
 
@@ -70,21 +71,26 @@ int launch_gemv_k(int cb, int V, int kc, const LinArgs& g, hipStream_t st) {
   }
 }
 
-template <int K, int CB, int V>
+template <int K, int CB, int V, int F16>
 static int launch_bgemm_nc(int nc, const LinArgs& g, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(g.total));
   switch (nc) {
-    case 1: hipLaunchKernelGGL((bgemm_kernel<K, CB, V, 1>), grid, dim3(64 * BG_WAVES), 0, st, g); break;
-    case 2: hipLaunchKernelGGL((bgemm_kernel<K, CB, V, 2>), grid, dim3(64 * BG_WAVES), 0, st, g); break;
-    case 4: hipLaunchKernelGGL((bgemm_kernel<K, CB, V, 4>), grid, dim3(64 * BG_WAVES), 0, st, g); break;
-    default: hipLaunchKernelGGL((bgemm_kernel<K, CB, V, 8>), grid, dim3(64 * BG_WAVES), 0, st, g); break;
+    case 1: hipLaunchKernelGGL((bgemm_kernel<K, CB, V, 1, F16>), grid, dim3(64 * BG_WAVES), 0, st, g); break;
+    case 2: hipLaunchKernelGGL((bgemm_kernel<K, CB, V, 2, F16>), grid, dim3(64 * BG_WAVES), 0, st, g); break;
+    case 4: hipLaunchKernelGGL((bgemm_kernel<K, CB, V, 4, F16>), grid, dim3(64 * BG_WAVES), 0, st, g); break;
+    default: hipLaunchKernelGGL((bgemm_kernel<K, CB, V, 8, F16>), grid, dim3(64 * BG_WAVES), 0, st, g); break;
   }
   return hipGetLastError() == hipSuccess ? 0 : 13;
 }
 
+template <int K, int CB, int V>
+static int launch_bgemm_f(int nc, const LinArgs& g, hipStream_t st) {
+  return g.mma_f16 ? launch_bgemm_nc<K, CB, V, 1>(nc, g, st) : launch_bgemm_nc<K, CB, V, 0>(nc, g, st);
+}
+
 template <int K, int CB>
 static int launch_bgemm_v(int V, int nc, const LinArgs& g, hipStream_t st) {
-  return V == 2 ? launch_bgemm_nc<K, CB, 2>(nc, g, st) : launch_bgemm_nc<K, CB, 1>(nc, g, st);
+  return V == 2 ? launch_bgemm_f<K, CB, 2>(nc, g, st) : launch_bgemm_f<K, CB, 1>(nc, g, st);
 }
 
 template <int K>

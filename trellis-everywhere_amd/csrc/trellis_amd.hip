@@ -139,18 +139,22 @@ int gemv_kr(const trellis_desc* const* W, int count) {
 
 // Batch >= 2 (bgemm_kernel): NC 16-column batch chunks per workgroup (up to 128 columns),
 // a work item is one 128-row block x one column block x one k-range of kr tile columns
-// (a multiple of the k-step, 8 tiles up to 64 columns, else 4), run by one 16-wave
-// workgroup per CU. kr minimises ceil(items/CUs) x the per-SIMD work of an item (2 bands
-// x kr tiles x (decode ~61 + NC MFMAs x ~19 cycles)) plus, with split-K, the bfold_kernel
+// (a multiple of the k-step: 8 tiles up to 64 columns and in the fp16-weight mode, else
+// 4), run by one 16-wave workgroup per CU. kr minimises ceil(items/CUs) x the per-SIMD work
+// of an item (2 bands x kr tiles x (decode ~61 + NC MFMAs x ~19 cycles; fp16-weight mode
+// ~75 + NC x ~10)) plus, with split-K, the bfold_kernel
 // launch (~1.5 us) and the partial blocks it moves (S x rows x NB x 4 bytes written and
 // read at ~2.5 KB per cycle), plus a start-up latency per round after the first.
 // TRELLIS_BGEMM_KR forces a value.
 int bgemm_nc(int batch) { return batch <= 16 ? 1 : batch <= 32 ? 2 : batch <= 64 ? 4 : 8; }
 
-int bgemm_kr(const trellis_desc* const* W, int count, int batch, int nc) {
+int bgemm_kr(const trellis_desc* const* W, int count, int batch, int nc, bool f16) {
   int maxt = 0;
   for (int i = 0; i < count; ++i) maxt = W[i]->k_in / 16 > maxt ? W[i]->k_in / 16 : maxt;
-  const int kt = nc <= 4 ? 8 : 4;
+  const int kt = (f16 || nc <= 4) ? 8 : 4;
+  // per band-tile SIMD cycles: the decode and NC MFMAs (the fp16-weight mode decodes a
+  // little more and issues half the MFMAs)
+  const long long tile_cost = f16 ? 75 + 10 * nc : 61 + 19 * nc;
   const int cap = ((maxt + kt - 1) / kt) * kt;
   const int forced = env_int("TRELLIS_BGEMM_KR", 0);
   if (forced >= kt && forced % kt == 0) return forced < cap ? forced : cap;
@@ -171,7 +175,7 @@ int bgemm_kr(const trellis_desc* const* W, int count, int batch, int nc) {
     if (smax > 16) continue;
     const long long rounds = (items + cus - 1) / cus;
     const long long epi = smax > 1 ? 3600 + 2 * part_bytes / 2500 : 0;
-    const long long cost = rounds * kr * 2 * (61 + 19 * nc) + epi + (rounds - 1) * 3600;
+    const long long cost = rounds * kr * 2 * tile_cost + epi + (rounds - 1) * 3600;
     if (best_cost < 0 || cost < best_cost) {
       best = kr;
       best_cost = cost;
@@ -180,13 +184,13 @@ int bgemm_kr(const trellis_desc* const* W, int count, int batch, int nc) {
   return best;
 }
 
-GroupPlan group_plan(const trellis_desc* const* W, int count, int batch) {
+GroupPlan group_plan(const trellis_desc* const* W, int count, int batch, bool f16) {
   GroupPlan p;
   p.gemv = batch == 1;
   p.nb = batch;
   p.nc = bgemm_nc(batch);
   p.ncb = p.gemv ? 1 : (batch + 16 * p.nc - 1) / (16 * p.nc);
-  p.kr = p.gemv ? gemv_kr(W, count) : bgemm_kr(W, count, batch, p.nc);
+  p.kr = p.gemv ? gemv_kr(W, count) : bgemm_kr(W, count, batch, p.nc, f16);
   p.kc = p.kr >= 32 ? 16 : 8;
   {
     const int kc = env_int("TRELLIS_GEMV_KC", 0);
@@ -343,6 +347,7 @@ const char* trellis_strerror(int status) {
     case TRELLIS_ERR_RANGE: return "tile range outside the matrix";
     case TRELLIS_ERR_LAUNCH: return "HIP kernel launch failed";
     case TRELLIS_ERR_GROUP: return "a group holds 1..8 linears sharing K, V and codebook";
+    case TRELLIS_ERR_FLAGS: return "unknown flag bits";
     default: return "unknown trellis status";
   }
 }
@@ -353,7 +358,9 @@ int trellis_workspace_bytes_group(const trellis_desc* const* W, int count, int b
   const int v = validate_group(W, count);
   if (v) return v;
   if (batch < 1) return TRELLIS_ERR_BATCH;
-  *bytes = group_plan(W, count, batch).ws;
+  // either MFMA mode's plan fits (their k-ranges, hence partial buffers, may differ)
+  const size_t a = group_plan(W, count, batch, false).ws, b = group_plan(W, count, batch, true).ws;
+  *bytes = a > b ? a : b;
   return TRELLIS_OK;
 }
 
@@ -362,8 +369,7 @@ int trellis_workspace_bytes(const trellis_desc* W, int batch, size_t* bytes) {
   const int v = validate(W);
   if (v) return v;
   if (batch < 1) return TRELLIS_ERR_BATCH;
-  *bytes = group_plan(&W, 1, batch).ws;
-  return TRELLIS_OK;
+  return trellis_workspace_bytes_group(&W, 1, batch, bytes);
 }
 
 int trellis_decode_tiles(const trellis_desc* W, uint32_t tile_begin, uint32_t ntiles, float* out,
@@ -450,12 +456,14 @@ int trellis_encode_tiles(const float* w, uint32_t ntiles, int K, int codebook, u
   }
 }
 
-int trellis_packed_linear_group(const trellis_desc* const* W, int count, const void* const* x,
-                                 const int64_t* ldx, int batch, int x_dtype, void* const* y,
-                                 const int64_t* ldy, int y_dtype, void* workspace,
-                                 size_t ws_bytes, void* stream) {
+int trellis_packed_linear_group_ex(const trellis_desc* const* W, int count, const void* const* x,
+                                   const int64_t* ldx, int batch, int x_dtype, void* const* y,
+                                   const int64_t* ldy, int y_dtype, void* workspace,
+                                   size_t ws_bytes, int flags, void* stream) {
   int v = validate_group(W, count);
   if (v) return v;
+  if (flags & ~TRELLIS_MMA_F16) return TRELLIS_ERR_FLAGS;
+  const bool f16 = (flags & TRELLIS_MMA_F16) != 0 && batch > 1;
   if (!x || !y || !ldx || !ldy) return TRELLIS_ERR_NULL;
   if (batch < 1) return TRELLIS_ERR_BATCH;
   if ((x_dtype != TRELLIS_F32 && x_dtype != TRELLIS_F16) ||
@@ -468,7 +476,7 @@ int trellis_packed_linear_group(const trellis_desc* const* W, int count, const v
     if (reinterpret_cast<uintptr_t>(x[i]) % 4) return TRELLIS_ERR_ALIGN;
     if (x_dtype == TRELLIS_F16 && batch > 1 && ldx[i] % 2) return TRELLIS_ERR_ALIGN;
   }
-  const GroupPlan p = group_plan(W, count, batch);
+  const GroupPlan p = group_plan(W, count, batch, f16);
   if (!workspace || ws_bytes < p.ws) return TRELLIS_ERR_WORKSPACE;
   if (reinterpret_cast<uintptr_t>(workspace) % 256) return TRELLIS_ERR_ALIGN;
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -481,6 +489,7 @@ int trellis_packed_linear_group(const trellis_desc* const* W, int count, const v
   g.x_f16 = x_dtype == TRELLIS_F16;
   g.y_f16 = y_dtype == TRELLIS_F16;
   g.kr = p.kr;
+  g.mma_f16 = f16;
   int item0 = 0;
   char* ws = static_cast<char*>(workspace);
   for (int i = 0; i < count; ++i) {
@@ -494,6 +503,7 @@ int trellis_packed_linear_group(const trellis_desc* const* W, int count, const v
     m.ldy = ldy[i];
     m.n = W[i]->n_out;
     m.k = W[i]->k_in;
+    m.xfw = f16 ? ((W[i]->k_in + 31) / 32) * 16 : W[i]->k_in;
     m.tiles_in = W[i]->k_in / 16;
     m.block_in = W[i]->block_in;
     m.block_out = W[i]->block_out;
@@ -521,7 +531,7 @@ int trellis_packed_linear_group(const trellis_desc* const* W, int count, const v
   if (env_int("TRELLIS_PLAN_LOG", 0))
     std::fprintf(stderr, "trellis plan: batch=%d members=%d mode=%s kr=%d kc=%d nc=%d ncb=%d "
                          "items=%d S0=%d ws=%zu\n",
-                 batch, count, p.gemv ? "gemv" : "bgemm", p.kr, p.kc, p.nc,
+                 batch, count, p.gemv ? "gemv" : f16 ? "bgemm-f16" : "bgemm", p.kr, p.kc, p.nc,
                  p.ncb, p.total, p.S[0], p.ws);
   const size_t xes = g.x_f16 ? 2 : 4, yes = g.y_f16 ? 2 : 4;
   for (int b0 = 0; b0 < batch; b0 += p.nb) {
@@ -540,11 +550,26 @@ int trellis_packed_linear_group(const trellis_desc* const* W, int count, const v
   return TRELLIS_OK;
 }
 
+int trellis_packed_linear_group(const trellis_desc* const* W, int count, const void* const* x,
+                                 const int64_t* ldx, int batch, int x_dtype, void* const* y,
+                                 const int64_t* ldy, int y_dtype, void* workspace,
+                                 size_t ws_bytes, void* stream) {
+  return trellis_packed_linear_group_ex(W, count, x, ldx, batch, x_dtype, y, ldy, y_dtype,
+                                        workspace, ws_bytes, 0, stream);
+}
+
+int trellis_packed_linear_ex(const trellis_desc* W, const void* x, int64_t ldx, int batch,
+                             int x_dtype, void* y, int64_t ldy, int y_dtype, void* workspace,
+                             size_t ws_bytes, int flags, void* stream) {
+  return trellis_packed_linear_group_ex(&W, 1, &x, &ldx, batch, x_dtype, &y, &ldy, y_dtype,
+                                        workspace, ws_bytes, flags, stream);
+}
+
 int trellis_packed_linear(const trellis_desc* W, const void* x, int64_t ldx, int batch,
                           int x_dtype, void* y, int64_t ldy, int y_dtype, void* workspace,
                           size_t ws_bytes, void* stream) {
-  return trellis_packed_linear_group(&W, 1, &x, &ldx, batch, x_dtype, &y, &ldy, y_dtype,
-                                     workspace, ws_bytes, stream);
+  return trellis_packed_linear_ex(W, x, ldx, batch, x_dtype, y, ldy, y_dtype, workspace,
+                                  ws_bytes, 0, stream);
 }
 
 }  // extern "C"
