@@ -1,6 +1,6 @@
 """Benchmark: trellis packed-linear decode-matmul on MI355X, Qwen3-8B block linears.
 
-Headline (BASELINE.json configs[2]): the seven linears of one Qwen3-8B decoder block,
+Headline: the seven linears of one Qwen3-8B decoder block,
 q 4096->4096, k/v 4096->1024, o 4096->4096, gate/up 4096->12288, down 12288->4096, K=3,
 MCG, V=1, packed bits uniform random from a seed, seeded +-1 signs, per-matrix scale,
 fp16 N(0,1) activations, batch 1. One step = the seven packed linears of one block in
@@ -14,7 +14,7 @@ n*k*K/8). The JSON line also carries us/layer, the dominant launch's HBM rooflin
 duration from HIP events on the launch stream), the same block at batch 64 with its fp16
 MFMA roofline (algorithmic 2*B*n*k flops), and a CPU baseline: this repo's torch-CPU
 restatement of the reference decode+restore+matmul (oracle/torch_cpu.py) on a bounded
-sample. --sweep adds BASELINE configs[4]: K=2,3,4 x V=1,2 on the gate/up/down shapes at
+sample. --sweep adds the sweep K=2,3,4 x V=1,2 on the gate/up/down shapes at
 batch 1 and at a 512-token prefill.
 """
 from __future__ import annotations
@@ -66,7 +66,7 @@ def traffic_from_profile(path=TRAFFIC_FILE):
 
 
 def make_layers(te, torch, dev, layers, K, V, seed, codebook="mcg"):
-    """Seeded synthetic packed linears on the device."""
+    """Seeded synthetic packed linears on the device (uniform random bits, seeded signs/scales)."""
     import numpy as np
     from_dev = te.PackedLinear.from_device
     g = torch.Generator(device=dev)
@@ -285,13 +285,13 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--batch", type=int, default=1, help="headline batch (BASELINE: 1)")
+    ap.add_argument("--batch", type=int, default=1, help="headline batch (default 1)")
     ap.add_argument("--K", type=int, default=3)
     ap.add_argument("--V", type=int, default=1)
     ap.add_argument("--no-batch64", action="store_true", help="skip the batch-64 MFMA figure")
     ap.add_argument("--mma-f16", action="store_true",
                     help="batch >= 2: the fp16-weight MFMA mode (TRELLIS_MMA_F16) for the block run")
-    ap.add_argument("--sweep", action="store_true", help="add BASELINE configs[4] (K x V sweep)")
+    ap.add_argument("--sweep", action="store_true", help="add the K x V sweep on the gate/up/down shapes")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the LM-head GEMV and embedding-row lookup figures")

@@ -328,7 +328,7 @@ def restore(zq: np.ndarray, scale, su, sv, in_s, out_s, block: int = 128) -> np.
 
 def w_hat_from_record(packed: np.ndarray, rec: IPRecord) -> np.ndarray:
     """restore(decode(bits)) from the packed words and stored f16/f32 metadata: the
-    definition the packed-linear call must match (SURVEY: y = restore(decode(bits)) @ x;
+    definition the packed-linear call must match (y = restore(decode(bits)) @ x;
     packed.js:51-52 folds scale into isc, which restore applies as zq*scale)."""
     zt = decode_packed_tiles(packed, rec.K, rec.codebook, rec.V)
     zq = tiles_to_matrix(zt, rec.n, rec.k)
@@ -376,7 +376,7 @@ def codebook_rms_v2(codebook: str) -> float:
 
 def synthetic_record(n: int, k: int, K: int, seed: int, codebook: str = "mcg",
                      mean1_scales: bool = True, V: int = 1):
-    """Seeded synthetic packed linear as BASELINE configs 2-5 describe: uniform random
+    """Seeded synthetic packed linear as the benchmark configurations use: uniform random
     u32 bits (every stream is a valid tail-biting path), ±1 su/sv, per-matrix scale
     fp16(0.02 / RMS_codebook) stored as f32, isc/osc mean-1 (or ones)."""
     rng = np.random.default_rng(seed)

@@ -2,7 +2,7 @@
 
 Restates the reference encoder src/trellis/qtip.py:124-196 (tail-biting Viterbi) and
 the layer path of scripts/export_packed.py:52-61 (IP -> tiles -> encode -> pack), used
-to build the config-1 fixture.
+to build the config-1 fixture (the SmolLM2-135M up_proj configuration).
 """
 from __future__ import annotations
 

@@ -1,13 +1,13 @@
 """Generate the committed golden fixtures under tests/golden/ (run from the repo root:
 ``python tests/golden/make_fixtures.py``). Inputs and expected outputs only.
 
-config1_smollm2_up.npz  BASELINE configs[0]: SmolLM2-135M MLP up_proj shape (576 -> 1536,
+config1_smollm2_up.npz  the CPU-runnable configuration: SmolLM2-135M MLP up_proj shape (576 -> 1536,
     torch weight [1536, 576]), W ~ N(0, 0.02) fp32 from seed 0, IP with seeded +-1 signs
     (numpy generator, seed 1), tail-biting Viterbi (oracle/viterbi.c, L=16, K=3, V=1,
     16x16 tiles, 3INST codebook), packed as export_packed.py:27-35. x: fp16 N(0,1) [2, 576]
     (seed 2). y_ref = W_hat @ x in float64 (oracle), W_hat = restore(decode(bits)).
-synth_K{K}_{cb}.npz  seeded synthetic records (uniform random bits
-    recipe) at 64 x 128 for K in {2,3,4} x {mcg,3inst,1mad}: the first 8 decoded tiles,
+synth_K{K}_{cb}.npz  seeded synthetic records (uniform random bits, the benchmark
+    configurations' recipe) at 64 x 128 for K in {2,3,4} x {mcg,3inst,1mad}: the first 8 decoded tiles,
     a sha256 of all decoded tiles, x [3, 128] fp16 and y_ref.
 """
 import hashlib

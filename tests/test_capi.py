@@ -114,7 +114,7 @@ def test_encode_tiles_rejects_before_launch(te):
 
 
 def test_workspace_plan_is_bounded(te):
-    """Workspace for the largest BASELINE shape stays small (partials of 128-row blocks)."""
+    """Workspace for the largest benchmark shape stays small (partials of 128-row blocks)."""
     lib = te.library()
     d = _desc(te, n_out=12288, k_in=4096)
     n = ctypes.c_size_t(0)
