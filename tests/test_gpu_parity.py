@@ -69,7 +69,7 @@ def test_decode_tiles_all_states_bit_exact(te, gpu_device, K, cb):
 
 # ------------------------------------------------------------------ packed linear
 def test_config1_golden(te, gpu_device):
-    """SmolLM2 up_proj 576->1536, K=3, 3INST, real Viterbi encode."""
+    """The CPU-runnable configuration: SmolLM2 up_proj 576->1536, K=3, 3INST, real Viterbi encode."""
     _say("[linear] config1 golden")
     d, rec = fixture("config1_smollm2_up")
     lin = make_linear(te, d["bits"], rec, gpu_device)
@@ -156,7 +156,7 @@ def _oracle_block_rows(bits, rec, ob, x):
 @pytest.mark.parametrize("name,n,k", [("q_proj", 4096, 4096), ("k_proj", 1024, 4096),
                                       ("gate_proj", 12288, 4096), ("down_proj", 4096, 12288)])
 def test_qwen3_8b_shapes_sampled_blocks(te, gpu_device, name, n, k):
-    """BASELINE configs[2] at full size: every output row checked would need a 50M
+    """The Qwen3-8B block shapes at full size: every output row checked would need a 50M
     weight dense oracle, so three 128-row blocks (first, middle, last) are checked
     exactly and the rest by linearity: f(a*x1 + b*x2) = a f(x1) + b f(x2)."""
     _say(f"[8B] {name} {n}x{k}")
@@ -208,7 +208,7 @@ def test_group_rejects_mixed_k(te, gpu_device):
 
 @pytest.mark.parametrize("n,k,batch", [(2048, 6144, 512), (1024, 2048, 300), (256, 512, 129)])
 def test_prefill_vs_oracle(te, gpu_device, n, k, batch):
-    """BASELINE configs[4] prefill shape class: the batched decode-once kernel over many
+    """The prefill shape class: the batched decode-once kernel over many
     column blocks (ragged last block), against the float64 oracle."""
     _say(f"[prefill] n={n} k={k} batch={batch}")
     bits, rec, W = _record_and_w_hat(n, k, 3, "mcg")
