@@ -290,7 +290,7 @@ def main():
     ap.add_argument("--V", type=int, default=1)
     ap.add_argument("--no-batch64", action="store_true", help="skip the batch-64 MFMA figure")
     ap.add_argument("--mma-f16", action="store_true",
-                    help="batch >= 2: the fp16-weight MFMA mode (TRELLIS_MMA_F16) for the block run")
+                    help="batch >= 5: the fp16-weight MFMA mode (TRELLIS_MMA_F16) for the block run")
     ap.add_argument("--sweep", action="store_true", help="add the K x V sweep on the gate/up/down shapes")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
@@ -404,7 +404,7 @@ def main():
         "config": {"workload": f"Qwen3-8B decoder-block linears (q,k,v,o,gate,up,down), K={K}, "
                                f"MCG, V={V}, batch {B}",
                    "batch": B, "K": K, "V": V, "codebook": "mcg",
-                   "mma_f16": bool(args.mma_f16 and B > 1),
+                   "mma_f16": bool(args.mma_f16 and B > 4),
                    "block_packed_bytes": block_bytes, "weight_copies": copies,
                    "rotated_bytes": block_bytes * copies,
                    "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),

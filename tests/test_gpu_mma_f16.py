@@ -8,7 +8,7 @@ multiplies it by the fp16 activation once. Bars:
     numpy's round-to-nearest-even cast, the folded activations rounded to fp16 as the
     kernels store them, float64 sums): <= 1e-4, far below the ~2e-4 the rounding itself
     moves the result, so a wrong pairing of tiles, halves or activations fails;
-  * batch 1 ignores the flag (bit-identical to the default call).
+  * batch 1 to 4 (the exact decode-GEMV) ignore the flag (bit-identical to the default call).
 """
 import functools
 import sys
@@ -75,11 +75,14 @@ def test_mma_f16_vs_oracle(te, gpu_device, n, k, K, cb, V, batch):
     x = np.random.default_rng(batch + k).standard_normal((batch, k)).astype(np.float16)
     xt = torch.from_numpy(x).to(gpu_device)
     y = lin(xt, mma_f16=True).cpu().numpy()
+    y0 = lin(xt).cpu().numpy()
     assert tn.rel_err(y, x.astype(np.float64) @ W.T) < TOL
+    if batch <= 4:
+        assert np.array_equal(y, y0)          # the exact decode-GEMV ignores the flag
+        return
     assert tn.rel_err(y, _emulated(rec, zq, x)) < TIGHT
     if cb != "1mad":
         # the mode is in effect: the exact default differs by the fp16 rounding
-        y0 = lin(xt).cpu().numpy()
         assert tn.rel_err(y, y0) > 1e-6
 
 
@@ -126,9 +129,10 @@ def test_mma_f16_dtypes(te, gpu_device):
     assert tn.rel_err(y16, x.astype(np.float64) @ W.T) < 2e-3
 
 
-def test_mma_f16_ignored_at_batch1(te, gpu_device):
+@pytest.mark.parametrize("batch", [1, 3])
+def test_mma_f16_ignored_by_the_gemv(te, gpu_device, batch):
     bits, rec, zq, W = _case(576, 1536, 3, "mcg", 1)
     lin = make_linear(te, bits, rec, gpu_device)
-    x = torch.from_numpy(np.random.default_rng(1).standard_normal(1536).astype(np.float16))
+    x = torch.from_numpy(np.random.default_rng(1).standard_normal((batch, 1536)).astype(np.float16))
     x = x.to(gpu_device)
     assert torch.equal(lin(x, mma_f16=True), lin(x))

@@ -285,3 +285,37 @@ def test_v2_linear_vs_oracle(te, gpu_device, n, k, K, cb, batch):
     x = np.random.default_rng(batch).standard_normal((batch, k)).astype(np.float16)
     y = lin(torch.from_numpy(x).to(gpu_device)).cpu().numpy()
     assert tn.rel_err(y, x.astype(np.float64) @ W.T) < TOL
+
+
+@pytest.mark.parametrize("n,k,K,cb", [(1536, 576, 3, "3inst"), (576, 1536, 3, "mcg"),
+                                      (2048, 6144, 3, "mcg"), (384, 1024, 4, "3inst"),
+                                      (208, 336, 3, "1mad")])
+@pytest.mark.parametrize("batch", [2, 3, 4])
+def test_small_batch_gemv_rows(te, gpu_device, n, k, K, cb, batch):
+    """Batch 2 to 4 run the decode-GEMV with the batch rows in the MFMA's B columns (the
+    same plan as batch 1): each output row is bit-identical to the batch-1 call on that
+    input row, and within 1e-3 of the oracle."""
+    _say(f"[small batch] n={n} k={k} K={K} cb={cb} batch={batch}")
+    bits, rec, W = _record_and_w_hat(n, k, K, cb)
+    lin = make_linear(te, bits, rec, gpu_device)
+    x = np.random.default_rng(3 * batch + n).standard_normal((batch, k)).astype(np.float16)
+    xt = torch.from_numpy(x).to(gpu_device)
+    y = lin(xt).cpu().numpy()
+    for b in range(batch):
+        assert np.array_equal(y[b], lin(xt[b]).cpu().numpy())
+    assert tn.rel_err(y, x.astype(np.float64) @ W.T) < TOL
+
+
+def test_small_batch_group_strided(te, gpu_device):
+    """A group at batch 3 with strided f32 inputs and f16 outputs through the decode-GEMV."""
+    shapes = [(512, 1024), (128, 1024), (384, 1024)]
+    cases = [_record_and_w_hat(nn, kk, 3, "mcg") for nn, kk in shapes]
+    lins = [make_linear(te, b, r, gpu_device) for b, r, _ in cases]
+    grp = te.PackedGroup(lins)
+    xs = np.random.default_rng(9).standard_normal((3, 1024 + 96)).astype(np.float32)
+    xt = torch.from_numpy(xs).to(gpu_device)[:, :1024]
+    outs = [torch.zeros((3, nn + 64), dtype=torch.float16, device=gpu_device)[:, :nn]
+            for nn, _ in shapes]
+    grp([xt] * 3, outs)
+    for o, (_, _, W) in zip(outs, cases):
+        assert tn.rel_err(o.float().cpu().numpy(), xs[:, :1024].astype(np.float64) @ W.T) < 2e-3

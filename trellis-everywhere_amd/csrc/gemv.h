@@ -1,9 +1,10 @@
-// gemv.h — batch-1 packed linear for gfx950: a pipelined decode-GEMV.
+// gemv.h — packed linear for batch 1 to 4 on gfx950: a pipelined decode-GEMV.
 //
 // The decode goes straight into the A operand of v_mfma_f32_16x16x32_f16 (the codebook's
 // fp16 pair (hi, lo) against a duplicated activation, fp32 accumulation: common.h),
 // organised for batch 1, where the decode's VALU work and fixed per-launch latencies, not
-// HBM, set the time:
+// HBM, set the time. The MFMA's 16 B columns carry NB <= 4 batch rows (column n = batch
+// row n; NB = 1 at batch 1), so a few rows cost about what one does:
 //
 //   * Work item = one matrix x one 128-row output block (8 bands of 16 rows) x one
 //     k-range of `kr` tile columns, run by one 16-wave workgroup (one per CU): waves w and
@@ -14,9 +15,9 @@
 //     LDS buffer and decoded from there, so no barrier is needed in the main loop.
 //   * Tiles are decoded GEMV_G at a time into separate A registers before their MFMAs are
 //     issued: a decode then never waits for an MFMA to release its operands.
-//   * The activation fold xf = Hb_k(isc_scaled * su * x) of the k-range is computed once
-//     per workgroup (its loads are issued before the packed words) and kept in LDS as
-//     (x, x) fp16 pairs.
+//   * The activation fold xf = Hb_k(isc_scaled * su * x) of the k-range (every batch row)
+//     is computed once per workgroup (its loads are issued before the packed words) and
+//     kept in LDS as (x, x) fp16 pairs.
 //   * The two k-halves are added in LDS. With one k-range (S == 1) wave 0 applies
 //     y = sv * osc * Hb_n(t) directly; with split-K it publishes the block's partial sum,
 //     takes a ticket, and the last workgroup of the block adds the partials in slice order
@@ -32,7 +33,7 @@ constexpr int GEMV_MAX_KR = 256;  // tile columns per k-range (4096 activations)
 constexpr int GEMV_PF = 2;        // pipeline stages in flight per wave
 constexpr int GEMV_G = 4;         // tiles decoded before their MFMAs are issued
 
-template <int K, int CB, int V, int KC, int PF>
+template <int K, int CB, int V, int KC, int PF, int NB>
 __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
   constexpr int NWK = 8 * K;                 // words per tile
   constexpr int SW = KC * NWK;               // words per wave-stage
@@ -41,10 +42,12 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
   constexpr int CPT = NWK / 4;               // chunks per tile
   constexpr int SWP = LOADS * 256;           // words per wave buffer: every lane's chunks
   constexpr int FCH = GEMV_MAX_KR * 16 / 128 / GEMV_WAVES;  // fold chunks per wave (max)
+  // folded activations of the NB batch rows, rows 8 mod 64 words apart (bank spread)
+  constexpr int XROW = NB > 1 ? GEMV_MAX_KR * 16 + 8 : GEMV_MAX_KR * 16;
   __shared__ __align__(16) uint32_t stg[GEMV_WAVES * SWP];
-  __shared__ __align__(16) uint32_t xs[GEMV_MAX_KR * 16];
-  __shared__ float tt[2][128];
-  __shared__ unsigned ready[GEMV_MAX_KR / 8];   // per 128-column chunk of xs: folded
+  __shared__ __align__(16) uint32_t xs[NB * XROW];
+  __shared__ float tt[2][NB][128];
+  __shared__ unsigned ready[GEMV_MAX_KR / 8];   // per 128-column chunk of xs: rows folded
   __shared__ unsigned nready;                    // chunks folded so far
   // the wave index is uniform: kept scalar, so per-wave choices are scalar branches
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -67,6 +70,7 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
   uint32_t* mystg = stg + wave * SWP;
   const int kcols = ntl * 16;
   const int nch = (kcols + 127) / 128;
+  const int nbv = NB > 1 ? min(NB, g.batch) : 1;     // batch rows of the call (<= NB)
 
   // ---- loads. All of them go through range-checked buffer resources: an index past the
   // block's rows, the k-range's columns or the band's tiles reads zeros without touching
@@ -78,8 +82,9 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
   const rsrc_t r_sv = make_rsrc(m.sv + ob * 128, rows * 4);
   const rsrc_t r_osc = make_rsrc(m.osc + ob * 128, rows * 4);
   const int xsh = g.x_f16 ? 1 : 2;                   // log2 bytes per activation
+  const unsigned ldx = NB > 1 ? static_cast<unsigned>(m.ldx) : 0u;
   const rsrc_t r_x = make_rsrc(static_cast<const char*>(m.x) + (static_cast<size_t>(c0) * 16 << xsh),
-                               static_cast<unsigned>(kcols) << xsh);
+                               ((nbv - 1) * ldx + static_cast<unsigned>(kcols)) << xsh);
   const rsrc_t r_su = make_rsrc(m.su + c0 * 16, kcols * 4);
   const rsrc_t r_isc = make_rsrc(m.isc + c0 * 16, kcols * 4);
   const rsrc_t r_bits = make_rsrc(m.bits + (static_cast<size_t>(band) * m.tiles_in + c0) * NWK,
@@ -91,7 +96,11 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
     so[h] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r_sv, o, 0, 0)) *
             __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r_osc, o, 0, 0));
   }
-  uint32_t fw[FCH][2];
+  // fold jobs: the k-range's 128-column chunks, chunk ch folded by wave ch % GEMV_WAVES
+  // for every batch row (spreading the (chunk, row) pairs over all the waves measured
+  // slower: every wave then folds before its first decode)
+  const int njobs = nch;
+  uint32_t fw[FCH][NB][2];
   float fsu[FCH][2], fis[FCH][2];
 #pragma unroll
   for (int f = 0; f < FCH; ++f) {
@@ -99,7 +108,12 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const unsigned e = ch < nch ? ch * 128 + lane + 64 * h : RSRC_OOB / 4;
-      fw[f][h] = __builtin_amdgcn_raw_buffer_load_b32(r_x, static_cast<int>(((e << xsh) & ~3u)), 0, 0);
+#pragma unroll
+      for (int n = 0; n < NB; ++n) {
+        // batch row n of the call (rows past it read zeros)
+        const unsigned en = n < nbv && ch < nch ? n * ldx + e : RSRC_OOB / 4;
+        fw[f][n][h] = __builtin_amdgcn_raw_buffer_load_b32(r_x, static_cast<int>(((en << xsh) & ~3u)), 0, 0);
+      }
       fsu[f][h] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r_su, static_cast<int>(e * 4), 0, 0));
       fis[f][h] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r_isc, static_cast<int>(e * 4), 0, 0));
     }
@@ -137,16 +151,21 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
       const int ch = wave + GEMV_WAVES * f;
       if (ch < nch) {
         const int e0 = ch * 128 + lane, e1 = e0 + 64;
-        // columns past the k-range loaded as zeros
-        float lo = act_value(fw[f][0], e0, g.x_f16) * (fsu[f][0] * fis[f][0]);
-        float hi = act_value(fw[f][1], e1, g.x_f16) * (fsu[f][1] * fis[f][1]);
-        fwht_chunk(lo, hi, m.block_in, lane);
-        xs[e0] = dup_half(lo * nrm);
-        xs[e1] = dup_half(hi * nrm);
-        // publish the chunk: its xs words are written before the flag
+        // columns past the k-range loaded as zeros; an f16 row stride is even, so the
+        // element's half within its word follows e
+#pragma unroll
+        for (int n = 0; n < NB; ++n) {
+          float lo = act_value(fw[f][n][0], e0, g.x_f16) * (fsu[f][0] * fis[f][0]);
+          float hi = act_value(fw[f][n][1], e1, g.x_f16) * (fsu[f][1] * fis[f][1]);
+          fwht_chunk(lo, hi, m.block_in, lane);
+          xs[n * XROW + e0] = dup_half(lo * nrm);
+          xs[n * XROW + e1] = dup_half(hi * nrm);
+        }
+        // publish the chunk (all its rows): its xs words are written before the count
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         if (lane == 0) {
-          __hip_atomic_store(&ready[ch], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          __hip_atomic_fetch_add(&ready[ch], static_cast<unsigned>(nbv), __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_WORKGROUP);
           __hip_atomic_fetch_add(&nready, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
       }
@@ -154,21 +173,21 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
   }
 #pragma unroll
   for (int b = 1; b < PF; ++b) load_stage(s_begin + b, R[b]);
-  // No barrier: a wave decodes a stage as soon as the chunks it covers are folded (each
-  // wait ends: every chunk's folding wave publishes it before it decodes anything); once
-  // a wave has seen every chunk folded it stops checking.
+  // No barrier: a wave decodes a stage as soon as the chunks it covers are folded for
+  // every batch row (each wait ends: every wave publishes its chunks before it decodes
+  // anything); once a wave has seen every chunk done it stops checking.
   bool all_ready = false;
   auto wait_chunks = [&](int s) {
     if (all_ready || s >= s_end) return;
     const unsigned done = __builtin_amdgcn_readfirstlane(
         __hip_atomic_load(&nready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
-    if (done >= static_cast<unsigned>(nch)) {
+    if (done >= static_cast<unsigned>(njobs)) {
       all_ready = true;
     } else {
       const int ca = (s * KC) >> 3, cb = min((s * KC + KC - 1) >> 3, nch - 1);
       for (int c = ca; c <= cb; ++c)
         while (__builtin_amdgcn_readfirstlane(__hip_atomic_load(
-                   &ready[c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) == 0u)
+                   &ready[c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) < static_cast<unsigned>(nbv))
           __builtin_amdgcn_s_sleep(1);
     }
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
@@ -178,6 +197,9 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
   // of stage s + PF is issued into the freed registers, then stage s is decoded
   const int r = lane & 15, gq = lane >> 4;
   const QuadPos qp = quad_pos_v<K, V>(r, gq);
+  // B column r of the MFMA is batch row r (columns past the call's repeat its last row;
+  // their outputs are not used)
+  const uint32_t* xsr = xs + (NB > 1 ? min(r, nbv - 1) * XROW : 0);
   float4_t acc = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
   half8_t Bv[GEMV_G];
   auto stage = [&](int s, u32x4_t (&src)[LOADS]) {
@@ -187,7 +209,7 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
       *reinterpret_cast<u32x4_t*>(mystg + 4 * (lane + 64 * q)) = src[q];
     load_stage(s + PF, src);
     wait_chunks(s);
-    const uint32_t* xst = xs + s * KC * 16 + 4 * gq;
+    const uint32_t* xst = xsr + s * KC * 16 + 4 * gq;
     // G tiles at a time: their LDS reads, then their decodes into separate A registers,
     // then their MFMAs on alternating accumulators, so a decode never waits for the
     // previous MFMA to release its operand registers
@@ -251,64 +273,86 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
   // the ring's last loads (stages past the end) are not consumed: let them land
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   acc += acc1;
-  // column 0 of C: lanes 0, 16, 32, 48 hold rows 4*gq + i of the band
-  if (r == 0) {
+  // column n of C (batch row n): lanes n, n + 16, n + 32, n + 48 hold rows 4*gq + i of
+  // the band
+  if (r < NB) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) tt[half][bl * 16 + 4 * gq + i] = acc[i];
+    for (int i = 0; i < 4; ++i) tt[half][r][bl * 16 + 4 * gq + i] = acc[i];
   }
   __syncthreads();
   if (wave != 0) return;
 
   // ---- wave 0: the two k-halves, then (split-K) publish, ticket, and in the last
-  // workgroup of the block the partials in slice order; then y = sv * osc * Hb_n(t)
-  float t0 = tt[0][lane] + tt[1][lane], t1 = tt[0][lane + 64] + tt[1][lane + 64];
+  // workgroup of the block the partials in slice order; then y = sv * osc * Hb_n(t), one
+  // batch row at a time
+  float t0[NB], t1[NB];
+#pragma unroll
+  for (int n = 0; n < NB; ++n) {
+    t0[n] = tt[0][n][lane] + tt[1][n][lane];
+    t1[n] = tt[0][n][lane + 64] + tt[1][n][lane + 64];
+  }
   if (m.S > 1) {
-    float* mypart = m.part + (static_cast<size_t>(ob) * m.S + sl) * 128;
-    __hip_atomic_store(mypart + lane, t0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(mypart + lane + 64, t1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // partial sums [block][slice][NB][128]
+    float* mypart = m.part + (static_cast<size_t>(ob) * m.S + sl) * NB * 128;
+#pragma unroll
+    for (int n = 0; n < NB; ++n) {
+      if (n < nbv) {
+        __hip_atomic_store(mypart + n * 128 + lane, t0[n], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(mypart + n * 128 + lane + 64, t1[n], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     unsigned prev = 0;
     if (lane == 0)
       prev = __hip_atomic_fetch_add(m.tickets + ob, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     prev = __builtin_amdgcn_readfirstlane(prev);
     if (prev != static_cast<unsigned>(m.S - 1)) return;
-    const float* obpart = m.part + static_cast<size_t>(ob) * m.S * 128;
-    t0 = 0.f;
-    t1 = 0.f;
-    for (int s0 = 0; s0 < m.S; s0 += 8) {
-      float q0[8], q1[8];
+    const float* obpart = m.part + static_cast<size_t>(ob) * m.S * NB * 128;
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const float* p = obpart + static_cast<size_t>(min(s0 + u, m.S - 1)) * 128;
-        q0[u] = __hip_atomic_load(p + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        q1[u] = __hip_atomic_load(p + lane + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
+    for (int n = 0; n < NB; ++n) {
+      t0[n] = 0.f;
+      t1[n] = 0.f;
+      if (n >= nbv) continue;
+      for (int s0 = 0; s0 < m.S; s0 += 8) {
+        float q0[8], q1[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        if (s0 + u < m.S) {
-          t0 += q0[u];
-          t1 += q1[u];
+        for (int u = 0; u < 8; ++u) {
+          const float* p = obpart + (static_cast<size_t>(min(s0 + u, m.S - 1)) * NB + n) * 128;
+          q0[u] = __hip_atomic_load(p + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          q1[u] = __hip_atomic_load(p + lane + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (s0 + u < m.S) {
+            t0[n] += q0[u];
+            t1[n] += q1[u];
+          }
         }
       }
     }
     if (lane == 0) __hip_atomic_store(m.tickets + ob, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  if (CB == CB_1MAD) {
-    t0 = t0 / 147.800537109375f;
-    t1 = t1 / 147.800537109375f;
-  }
-  fwht_chunk(t0, t1, m.block_out, lane);
   const float nrm = m.nrm_out;
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int rl = lane + 64 * h;
-    if (rl < rows) {
-      const float v = (h ? t1 : t0) * nrm * so[h];
-      const long long o = ob * 128 + rl;
-      if (g.y_f16)
-        static_cast<_Float16*>(m.y)[o] = static_cast<_Float16>(v);
-      else
-        static_cast<float*>(m.y)[o] = v;
+  for (int n = 0; n < NB; ++n) {
+    if (n >= nbv) break;
+    float a = t0[n], b = t1[n];
+    if (CB == CB_1MAD) {
+      a = a / 147.800537109375f;
+      b = b / 147.800537109375f;
+    }
+    fwht_chunk(a, b, m.block_out, lane);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int rl = lane + 64 * h;
+      if (rl < rows) {
+        const float v = (h ? b : a) * nrm * so[h];
+        const long long o = (NB > 1 ? n * m.ldy : 0) + ob * 128 + rl;
+        if (g.y_f16)
+          static_cast<_Float16*>(m.y)[o] = static_cast<_Float16>(v);
+        else
+          static_cast<float*>(m.y)[o] = v;
+      }
     }
   }
 }

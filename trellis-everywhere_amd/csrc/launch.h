@@ -11,7 +11,9 @@
 
 namespace trellis {
 
-// gemv_kernel<K, cb, V, kc> over g.total items (batch 1, k-ranges of g.kr tiles).
+// gemv_kernel<K, cb, V, kc, nb> over g.total items (batch g.batch <= GEMV_MAX_NB, nb the
+// smallest of 1, 2, 4 that holds it; k-ranges of g.kr tiles).
+constexpr int GEMV_MAX_NB = 4;
 template <int K>
 int launch_gemv_k(int cb, int V, int kc, const LinArgs& g, hipStream_t st);
 
@@ -47,14 +49,21 @@ int launch_bfold(int cb, int nc, int nfold, const LinArgs& g, hipStream_t st) {
 #endif
 
 #ifdef TRELLIS_KERNELS_INSTANTIATE
-template <int K, int CB, int V>
-static int launch_gemv_kc(int kc, const LinArgs& g, hipStream_t st) {
+template <int K, int CB, int V, int NB>
+static int launch_gemv_nb(int kc, const LinArgs& g, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(g.total));
   if (kc == 8)
-    hipLaunchKernelGGL((gemv_kernel<K, CB, V, 8, GEMV_PF>), grid, dim3(64 * GEMV_WAVES), 0, st, g);
+    hipLaunchKernelGGL((gemv_kernel<K, CB, V, 8, GEMV_PF, NB>), grid, dim3(64 * GEMV_WAVES), 0, st, g);
   else
-    hipLaunchKernelGGL((gemv_kernel<K, CB, V, 16, GEMV_PF>), grid, dim3(64 * GEMV_WAVES), 0, st, g);
+    hipLaunchKernelGGL((gemv_kernel<K, CB, V, 16, GEMV_PF, NB>), grid, dim3(64 * GEMV_WAVES), 0, st, g);
   return hipGetLastError() == hipSuccess ? 0 : 13;
+}
+
+template <int K, int CB, int V>
+static int launch_gemv_kc(int kc, const LinArgs& g, hipStream_t st) {
+  if (g.batch <= 1) return launch_gemv_nb<K, CB, V, 1>(kc, g, st);
+  if (g.batch == 2) return launch_gemv_nb<K, CB, V, 2>(kc, g, st);
+  return launch_gemv_nb<K, CB, V, GEMV_MAX_NB>(kc, g, st);
 }
 
 template <int K, int CB>

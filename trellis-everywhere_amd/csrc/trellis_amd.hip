@@ -1,6 +1,6 @@
 // trellis_amd.hip — C ABI (include/trellis_amd.h): validation, launch planning, the
 // bit-exact tile decode kernel and the dispatch to the decode-matmul kernels (gemv_kernel at
-// batch 1, xfold_kernel + bgemm_kernel (+ bfold_kernel) above).
+// batch 1 to 4, xfold_kernel + bgemm_kernel (+ bfold_kernel) above).
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -102,7 +102,7 @@ int device_cus() {
   return cus;
 }
 
-// Batch 1 (gemv_kernel): a work item is one 128-row output block x one k-range of kr tile
+// Batch 1 to 4 (gemv_kernel): a work item is one 128-row output block x one k-range of kr tile
 // columns (kr a multiple of 8, so a k-range holds whole 128-column fold chunks), run by one
 // 16-wave workgroup; one workgroup fits a CU. kr minimises an estimate of the launch time in
 // 2.4 GHz cycles: rounds of items over the CUs x the decode of 8 bands x kr/2 tiles per wave
@@ -186,7 +186,7 @@ int bgemm_kr(const trellis_desc* const* W, int count, int batch, int nc, bool f1
 
 GroupPlan group_plan(const trellis_desc* const* W, int count, int batch, bool f16) {
   GroupPlan p;
-  p.gemv = batch == 1;
+  p.gemv = batch <= GEMV_MAX_NB;
   p.nb = batch;
   p.nc = bgemm_nc(batch);
   p.ncb = p.gemv ? 1 : (batch + 16 * p.nc - 1) / (16 * p.nc);
@@ -199,7 +199,8 @@ GroupPlan group_plan(const trellis_desc* const* W, int count, int batch, bool f1
   p.total = 0;
   p.folds = 0;
   p.ws = 0;
-  const int part_cols = p.gemv ? 1 : 16 * p.nc;
+  // partial sums per (block, slice): the gemv's 1, 2 or 4 batch rows, or bgemm's 16 * NC
+  const int part_cols = p.gemv ? (batch == 1 ? 1 : batch == 2 ? 2 : GEMV_MAX_NB) : 16 * p.nc;
   for (int i = 0; i < count; ++i) {
     p.n_ob[i] = (W[i]->n_out + 127) / 128;
     p.S[i] = (W[i]->k_in / 16 + p.kr - 1) / p.kr;
@@ -220,7 +221,7 @@ GroupPlan group_plan(const trellis_desc* const* W, int count, int batch, bool f1
   return p;
 }
 
-// Batch 1: the pipelined decode-GEMV (its x fold is fused).
+// Batch 1 to 4: the pipelined decode-GEMV (its x fold is fused).
 int launch_gemv(int K, int cb, int V, int kc, const LinArgs& g, hipStream_t st) {
   switch (K) {
     case 2: return launch_gemv_k<2>(cb, V, kc, g, st);
@@ -229,7 +230,7 @@ int launch_gemv(int K, int cb, int V, int kc, const LinArgs& g, hipStream_t st) 
   }
 }
 
-// The x fold of every member (batch > 1), written once to the workspace.
+// The x fold of every member (batch > 4), written once to the workspace.
 int launch_xfold(LinArgs& g, int folds, hipStream_t st) {
   const int items = g.total;
   g.total = folds;
@@ -463,7 +464,8 @@ int trellis_packed_linear_group_ex(const trellis_desc* const* W, int count, cons
   int v = validate_group(W, count);
   if (v) return v;
   if (flags & ~TRELLIS_MMA_F16) return TRELLIS_ERR_FLAGS;
-  const bool f16 = (flags & TRELLIS_MMA_F16) != 0 && batch > 1;
+  // the flag concerns the batched MFMA kernel only (the decode-GEMV is exact)
+  const bool f16 = (flags & TRELLIS_MMA_F16) != 0 && batch > GEMV_MAX_NB;
   if (!x || !y || !ldx || !ldy) return TRELLIS_ERR_NULL;
   if (batch < 1) return TRELLIS_ERR_BATCH;
   if ((x_dtype != TRELLIS_F32 && x_dtype != TRELLIS_F16) ||
