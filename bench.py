@@ -379,6 +379,14 @@ def main():
     if not args.no_extras and B == 1:
         log("[bench] extras: LM head (K=4) and embedding rows")
         extra = extras(te, torch, dev, max(40, args.steps // 5))
+        # small decode batches (the decode-GEMV carries up to 4 rows in its MFMA columns)
+        small = {}
+        for bs in (2, 4):
+            ssec_b, _, _, _ = run_block(te, torch, dev, LAYERS, GROUPS, bs, K, V,
+                                        max(20, args.steps // 5), max(3, args.warmup // 5),
+                                        per_launch=False)
+            small[str(bs)] = round(ssec_b * 1e6, 2)
+        extra["us_per_block_small_batch"] = small
         log(f"[bench] extras {extra}")
 
     # known-size copy for the HBM-counter scale factor (FETCH_SIZE / WRITE_SIZE)
