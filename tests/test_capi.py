@@ -84,6 +84,19 @@ def test_packed_linear_ex_flags(te):
     assert te._capi.MMA_F16 == 1
 
 
+def test_activation_range_limit(te):
+    """A call whose activations span 2 GiB or more (batch x row stride x element size) is
+    rejected on the host: the kernels address them through 32-bit byte ranges."""
+    lib = te.library()
+    d = _desc(te)
+    arr = (ctypes.POINTER(te._capi.TrellisDesc) * 1)(ctypes.pointer(d))
+    xp = (ctypes.c_void_p * 1)(16)
+    ld = (ctypes.c_int64 * 1)(1 << 22)
+    ldy = (ctypes.c_int64 * 1)(128)
+    # 256 rows x 4M f32 elements = 4 GiB
+    assert lib.trellis_packed_linear_group(arr, 1, xp, ld, 256, 0, xp, ldy, 0, None, 0, None) == 2
+
+
 def test_embed_rows_rejects_before_launch(te):
     """trellis_embed_rows validates on the host: descriptor, token count, pointers, dtype
     and row stride (web/packed.js:137-146 has no error path)."""

@@ -137,11 +137,12 @@ __global__ __launch_bounds__(64 * BG_WAVES) void bgemm_kernel(LinArgs g) {
     const int n = ch / RCH, off = ch % RCH;        // batch row, 16-byte chunk of its row
     xoff[q] = ch < XCH ? static_cast<unsigned>((n * m.xfw + c0 * WPT + off * 4) * 4) : RSRC_OOB;
   }
-  // packed words from the block's first band to the end of the matrix (bands past the
-  // matrix read zeros); lane chunk -> (band of the pair, tile of the k-lane, chunk)
+  // packed words of the block's bands (bands past the matrix read zeros; the range stays
+  // far below 4 GB whatever the matrix); lane chunk -> (band of the pair, tile of the
+  // k-lane, chunk)
   const size_t blk0 = static_cast<size_t>(ob) * 8 * m.tiles_in * NWK;
-  const rsrc_t r_b = make_rsrc(m.bits + blk0,
-                               static_cast<unsigned>((static_cast<size_t>(m.n / 16) * m.tiles_in * NWK - blk0) * 4));
+  const int nbands = min(8, m.n / 16 - ob * 8);    // bands of this block in the matrix
+  const rsrc_t r_b = make_rsrc(m.bits + blk0, static_cast<unsigned>(nbands * m.tiles_in * NWK * 4));
   unsigned boff[BLOADS];
 #pragma unroll
   for (int q = 0; q < BLOADS; ++q) {

@@ -477,6 +477,10 @@ int trellis_packed_linear_group_ex(const trellis_desc* const* W, int count, cons
     // activations are read as aligned u32 words
     if (reinterpret_cast<uintptr_t>(x[i]) % 4) return TRELLIS_ERR_ALIGN;
     if (x_dtype == TRELLIS_F16 && batch > 1 && ldx[i] % 2) return TRELLIS_ERR_ALIGN;
+    // the kernels address a call's activations through 32-bit byte ranges
+    const int64_t xes = x_dtype == TRELLIS_F16 ? 2 : 4;
+    if (static_cast<int64_t>(batch) * (batch > 1 ? ldx[i] : W[i]->k_in) * xes >= (int64_t(1) << 31))
+      return TRELLIS_ERR_SHAPE;
   }
   const GroupPlan p = group_plan(W, count, batch, f16);
   if (!workspace || ws_bytes < p.ws) return TRELLIS_ERR_WORKSPACE;
