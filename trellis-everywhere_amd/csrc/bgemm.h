@@ -194,11 +194,15 @@ __global__ __launch_bounds__(64 * BG_WAVES) void bgemm_kernel(LinArgs g) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int st = s + h;
-      // this wave's packed words of step st to its LDS buffer, then refill the slot with
-      // step st + 2 (the B part of that slot was stored to LDS one step earlier)
+      // this wave's packed words of step st to its LDS buffer; the B tile of step st + 1
+      // (loaded a step ago) to the other buffer, whose step st - 1 every wave finished
+      // before the last barrier: its stores drain while this step computes, instead of
+      // all waves' stores queueing in front of the barrier; then refill the slots with
+      // step st + 2 (the B part of this slot went to LDS a step earlier)
 #pragma unroll
       for (int q = 0; q < BLOADS; ++q)
         *reinterpret_cast<u32x4_t*>(mystg + 4 * (lane + 64 * q)) = br[h][q];
+      store_b(h ^ 1, xr[h ^ 1]);
       load_step(st + 2, xr[h], br[h]);
       if (st < nsteps) {
         const uint32_t* xb = xsb + h * XBUF + r * XW + 4 * gq;
@@ -240,9 +244,7 @@ __global__ __launch_bounds__(64 * BG_WAVES) void bgemm_kernel(LinArgs g) {
           }
         }
       }
-      // the B tile of step st + 1 (loaded a step ago) to the other buffer; the barrier
-      // also tells every wave that this buffer's step is done
-      store_b(h ^ 1, xr[h ^ 1]);
+      // every wave is done with this step's buffer, and the next step's B is stored
       __syncthreads();
     }
   }
