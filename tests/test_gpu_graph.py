@@ -1,0 +1,68 @@
+"""The packed linear inside captured HIP graphs (what bench.py times): every replay, with new
+inputs copied in and eager calls of the same linears between the replays, must equal the
+eager call on the same inputs bit for bit. Covers the batch-1 split-K tickets (reset by the
+kernels, no memset in the graph), the batch 2-4 decode-GEMV, the batched path with its
+x-fold and split-K fold launches, and the fp16-weight mode."""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import trellis_np as tn
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def make_linear(te, bits, rec, device):
+    r = te.PackedRecord(rec.n, rec.k, rec.K, bits, rec.su, rec.sv, rec.isc, rec.osc,
+                        float(rec.scale), codebook=rec.codebook, V=rec.V)
+    return te.PackedLinear(r, device=device)
+
+
+@pytest.mark.parametrize("batch,mma_f16", [(1, False), (3, False), (64, False), (64, True)])
+def test_graph_replays_match_eager(te, gpu_device, batch, mma_f16):
+    _say(f"[graph] batch={batch} mma_f16={mma_f16}")
+    shapes = [(1024, 2048), (256, 2048), (512, 2048)]      # split-K plans at every batch
+    lins = []
+    for i, (n, k) in enumerate(shapes):
+        bits, rec = tn.synthetic_record(n, k, 3, seed=40 + i)
+        lins.append(make_linear(te, bits, rec, gpu_device))
+    grp = te.PackedGroup(lins)
+    single = lins[0]
+    rng = np.random.default_rng(batch)
+    x = torch.from_numpy(rng.standard_normal((batch, 2048)).astype(np.float16)).to(gpu_device)
+    ys = [torch.empty((batch, n), device=gpu_device) for n, _ in shapes]
+    y1 = torch.empty((batch, shapes[0][0]), device=gpu_device)
+
+    def step():
+        grp([x] * 3, ys, mma_f16=mma_f16)
+        single.forward(x, out=y1, mma_f16=mma_f16)
+
+    step()                                   # workspaces allocated before the capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream(device=gpu_device)
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    with torch.cuda.graph(g):
+        step()
+    torch.cuda.synchronize()
+    for rep in range(4):
+        xin = torch.from_numpy(rng.standard_normal((batch, 2048)).astype(np.float16)).to(gpu_device)
+        x.copy_(xin)
+        g.replay()
+        torch.cuda.synchronize()
+        got = [y.clone() for y in ys] + [y1.clone()]
+        # eager calls on the same input (other outputs, same workspaces) between replays
+        want = grp([xin] * 3, mma_f16=mma_f16) + [single(xin, mma_f16=mma_f16)]
+        torch.cuda.synchronize()
+        for a, b in zip(got, want):
+            assert torch.equal(a, b), f"replay {rep}"
