@@ -276,7 +276,7 @@ def test_v2_decode_tiles_bit_exact(te, gpu_device, K, cb):
 
 @pytest.mark.parametrize("n,k,K,cb", [(256, 512, 3, "mcg"), (1536, 576, 2, "3inst"),
                                       (384, 2048, 4, "1mad"), (2048, 4096, 3, "mcg")])
-@pytest.mark.parametrize("batch", [1, 5, 64])
+@pytest.mark.parametrize("batch", [1, 2, 3, 5, 64])
 def test_v2_linear_vs_oracle(te, gpu_device, n, k, K, cb, batch):
     _say(f"[v2 linear] n={n} k={k} K={K} cb={cb} batch={batch}")
     bits, rec = tn.synthetic_record(n, k, K, seed=n + k + K, codebook=cb, V=2)
