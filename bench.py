@@ -179,6 +179,8 @@ def cpu_baseline(budget_s: float = 20.0):
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
+    log(f"[bench] cpu baseline on {cores} threads")
+    log(torch.__config__.parallel_info())
     n, k = 4096, 4096
     bits, rec = tn.synthetic_record(n, k, 3, seed=7)
     lut = tc.codebook_lut_torch("mcg")
