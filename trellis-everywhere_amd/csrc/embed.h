@@ -8,8 +8,11 @@
 // per (token, column block): one workgroup per (token, column block), 4 waves.
 //   * wave w takes the bands b = w, w + 4, ... of the row block; lane (row rl = l%16,
 //     column group g = l/16) decodes 4 weights of each tile (the same window/codebook
-//     code as the matmul kernels, exact fp32 values) and accumulates sign(rr, 16b + rl)
-//     * w per column, so a lane holds 4 columns of each of the block's tile columns;
+//     code as the matmul kernels) and accumulates sign(rr, 16b + rl) * w per column, so a
+//     lane holds 4 columns of each of the block's tile columns. MCG/3INST: one
+//     v_dot2_f32_f16 of the raw (hi, lo) fp16 pair with (sign, sign) per weight (the
+//     products are exact; hi + lo is the reference's exact fp32 sum); 1MAD: the integer
+//     (y - 510) * sign, exact in fp32, divided by 147.800537109375 once per output;
 //   * the 16 rows of a lane group are summed by DPP butterflies (all-reduce within a
 //     16-lane row), the 4 waves' column sums are added in LDS in wave order;
 //   * wave 0 applies the column-side Hadamard (fwht_chunk) and the scales.
@@ -57,6 +60,7 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
   for (int b = wave; b < nbands; b += 4) {
     const int c = 16 * b + rl;                       // row within the row block
     const float sgn = (__builtin_popcount(rr & c) & 1) ? -1.f : 1.f;
+    const half2_t s2 = {static_cast<_Float16>(sgn), static_cast<_Float16>(sgn)};
     const uint32_t* band = a.bits + (static_cast<size_t>(rb / 16 + b) * a.tiles_in + jb / 16) * NWK;
 #pragma unroll
     for (int tc = 0; tc < 8; ++tc) {
@@ -65,7 +69,13 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
         uint32_t raw[4];
         decode_quad<K, CB, V>(tp[qp.wa], tp[qp.wb], qp.sh, raw);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) acc[tc][q] += sgn * cb_exact<CB>(raw[q]);
+        for (int q = 0; q < 4; ++q) {
+          if constexpr (CB == CB_1MAD)
+            acc[tc][q] += sgn * static_cast<float>(static_cast<int>(raw[q]) - 510);
+          else
+            acc[tc][q] = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, raw[q]), s2,
+                                                acc[tc][q], false);
+        }
       }
     }
   }
@@ -95,6 +105,10 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
   for (int w = 0; w < nw; ++w) {
     if (lane < a.block_in) lo += colsum[w][lane];
     if (lane + 64 < a.block_in) hi += colsum[w][lane + 64];
+  }
+  if (CB == CB_1MAD) {
+    lo = lo / 147.800537109375f;
+    hi = hi / 147.800537109375f;
   }
   fwht_chunk(lo, hi, a.block_in, lane);
   const float rs = ok ? a.sv[r] * a.osc[r] * a.nrm : 0.f;
