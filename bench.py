@@ -104,11 +104,12 @@ def capture(torch, fn):
 
 
 def run_block(te, torch, dev, layers, groups, B, K, V, steps, warmup, min_bytes=1.0e9,
-              per_launch=True, mma_f16=False):
+              per_launch=True, mma_f16=False, copies=None):
     """Time `steps` replays of the block (its launches in order) over distinct weight copies.
     Returns (seconds per step, {group: us per launch}, {layer: us per launch})."""
     block_bytes = sum(n * k * K // 8 for _, n, k in layers)
-    copies = max(2, math.ceil(min_bytes / block_bytes))
+    if copies is None:
+        copies = max(2, math.ceil(min_bytes / block_bytes))
     blocks = [make_layers(te, torch, dev, layers, K, V, seed=c) for c in range(copies)]
     kin = {name: k for name, _, k in layers}
     xs = {name: torch.randn((B, kin[name]), device=dev, dtype=torch.float16) for name, _, _ in layers}
@@ -291,6 +292,9 @@ def main():
     ap.add_argument("--K", type=int, default=3)
     ap.add_argument("--V", type=int, default=1)
     ap.add_argument("--no-batch64", action="store_true", help="skip the batch-64 MFMA figure")
+    ap.add_argument("--weight-copies", type=int, default=None,
+                    help="distinct weight copies the steps rotate over (default: >= 1 GB of "
+                         "packed bits, beyond the 256 MB MALL; 1 keeps a block resident in it)")
     ap.add_argument("--mma-f16", action="store_true",
                     help="batch >= 5: the fp16-weight MFMA mode (TRELLIS_MMA_F16) for the block run")
     ap.add_argument("--sweep", action="store_true", help="add the K x V sweep on the gate/up/down shapes")
@@ -314,7 +318,8 @@ def main():
 
     log(f"[bench] block batch {B} K={K} V={V}")
     sec, us_group, us_layer, copies = run_block(te, torch, dev, LAYERS, GROUPS, B, K, V,
-                                                args.steps, args.warmup, mma_f16=args.mma_f16)
+                                                args.steps, args.warmup, mma_f16=args.mma_f16,
+                                                copies=args.weight_copies)
     gbs = block_bytes / sec / 1e9
     dom_us = us_group[DOMINANT]
     dom_bytes = 2 * 12288 * 4096 * K // 8
