@@ -134,3 +134,14 @@ def test_workspace_plan_is_bounded(te):
     for b in (1, 2, 8, 64):
         assert lib.trellis_workspace_bytes(ctypes.byref(d), b, ctypes.byref(n)) == 0
         assert n.value < 64 << 20
+
+
+def test_packed_linear_lives_on_a_gpu(te):
+    """A packed linear on a host device is refused at construction: the kernels would
+    dereference its pointers on the GPU."""
+    from oracle import trellis_np as tn
+    bits, rec = tn.synthetic_record(64, 128, 3, seed=1)
+    r = te.PackedRecord(rec.n, rec.k, rec.K, bits, rec.su, rec.sv, rec.isc, rec.osc,
+                        float(rec.scale), codebook=rec.codebook, V=rec.V)
+    with pytest.raises(ValueError):
+        te.PackedLinear(r, device="cpu")

@@ -13,7 +13,7 @@ from .format import PackedRecord, fit_block, read_packed, write_packed
 
 __all__ = ["PackedRecord", "read_packed", "write_packed", "fit_block", "TrellisError",
            "TrellisLibraryMissing", "PackedLinear", "PackedGroup", "PackedOps", "load_packed",
-           "encode_tiles", "library"]
+           "encode_tiles", "library", "TrellisLinear", "TrellisGroupLinear", "swap_linears"]
 
 
 def library():
@@ -26,4 +26,7 @@ def __getattr__(name):
     if name in ("PackedLinear", "PackedGroup", "PackedOps", "load_packed", "encode_tiles"):
         from . import packed_linear
         return getattr(packed_linear, name)
+    if name in ("TrellisLinear", "TrellisGroupLinear", "swap_linears"):
+        from . import modules
+        return getattr(modules, name)
     raise AttributeError(name)

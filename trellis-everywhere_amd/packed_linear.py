@@ -57,6 +57,9 @@ class PackedLinear:
         self.block_in, self.block_out = fit_block(self.k_in), fit_block(self.n_out)
         self.nwords = (256 * self.K + 31) // 32
         self.device = bits.device
+        if self.device.type != "cuda":
+            # the kernels dereference these pointers on the GPU
+            raise ValueError(f"a packed linear lives on a GPU device, not {self.device}")
         ntiles = (self.n_out // 16) * (self.k_in // 16)
         if tuple(bits.shape) != (ntiles, self.nwords) or not bits.is_contiguous():
             raise ValueError(f"bits must be contiguous [{ntiles}, {self.nwords}]")
