@@ -11,8 +11,8 @@ HBM; to defeat the 256 MB Infinity Cache the steps rotate over `copies` distinct
 
 value = packed-weight bytes of the block / seconds per step (GB/s, algorithmic bytes
 n*k*K/8). The JSON line also carries us/layer, the dominant launch's HBM roofline (gate+up,
-duration from HIP events on the launch stream), the same block at batch 64 with its fp16
-MFMA roofline (algorithmic 2*B*n*k flops), and a CPU baseline: this repo's torch-CPU
+duration from HIP events on the launch stream), the same block at batch 16 and 64 with
+their fp16 MFMA rooflines (algorithmic 2*B*n*k flops), and a CPU baseline: this repo's torch-CPU
 restatement of the reference decode+restore+matmul (oracle/torch_cpu.py) on a bounded
 sample. --sweep adds the sweep K=2,3,4 x V=1,2 on the gate/up/down shapes at
 batch 1 and at a 512-token prefill.
@@ -283,6 +283,44 @@ def block_flops(layers, B):
     return sum(2 * B * n * k for _, n, k in layers)
 
 
+def batched_figure(te, torch, dev, bs, K, V, args):
+    """The block at batch `bs` through the batched MFMA path (x fold, decode-to-MFMA GEMM,
+    split-K fold), exact and in the fp16-weight mode, with the gate+up launch's fp16 MFMA
+    roofline (algorithmic 2*bs*n*k flops over the launch, launch gap included)."""
+    log(f"[bench] block batch {bs}")
+    steps, warmup = max(20, args.steps // 10), max(3, args.warmup // 5)
+    sec, grp, _, _ = run_block(te, torch, dev, LAYERS, GROUPS, bs, K, V, steps, warmup,
+                               per_launch=True)
+    fl = block_flops(LAYERS, bs)
+    dom_fl = 2 * bs * 2 * 12288 * 4096
+    dom_tf = dom_fl / (grp[DOMINANT] * 1e-6) / 1e12
+    nc = 1 if bs <= 16 else 2 if bs <= 32 else 4 if bs <= 64 else 8
+    out = {"us_per_block": round(sec * 1e6, 2),
+           "tflops": round(fl / sec / 1e12, 2),
+           "mfma_frac_of_fp16_peak": round(fl / sec / 1e12 / MFMA_FP16_PEAK_TFLOPS, 4),
+           "us_per_group_launch": grp,
+           "roofline": {"bound": "mfma", "achieved": round(dom_tf, 2),
+                        "peak": MFMA_FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                        "frac": round(dom_tf / MFMA_FP16_PEAK_TFLOPS, 4),
+                        "kernel": f"bgemm_kernel<K={K},MCG,V={V},NC={nc}> (+xfold, bfold) "
+                                  f"on gate+up at batch {bs}",
+                        "avg_launch_us": grp[DOMINANT],
+                        "algorithmic_flops_per_launch": dom_fl}}
+    log(f"[bench] batch {bs}: {out['us_per_block']} us/block, {out['tflops']} TFLOP/s")
+    # the same block with the fp16-weight MFMA mode (each codebook value rounded once
+    # to fp16, one MAC per weight; max rel err ~2-3e-4 against the exact default)
+    sech, grph, _, _ = run_block(te, torch, dev, LAYERS, GROUPS, bs, K, V, steps, warmup,
+                                 per_launch=True, mma_f16=True)
+    out["mma_f16"] = {"us_per_block": round(sech * 1e6, 2),
+                      "tflops": round(fl / sech / 1e12, 2),
+                      "mfma_frac_of_fp16_peak": round(fl / sech / 1e12 / MFMA_FP16_PEAK_TFLOPS, 4),
+                      "us_per_group_launch": grph,
+                      "gate_up_tflops": round(dom_fl / (grph[DOMINANT] * 1e-6) / 1e12, 2)}
+    log(f"[bench] batch {bs} mma_f16: {out['mma_f16']['us_per_block']} us/block, "
+        f"{out['mma_f16']['tflops']} TFLOP/s")
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -291,7 +329,7 @@ def main():
     ap.add_argument("--batch", type=int, default=1, help="headline batch (default 1)")
     ap.add_argument("--K", type=int, default=3)
     ap.add_argument("--V", type=int, default=1)
-    ap.add_argument("--no-batch64", action="store_true", help="skip the batch-64 MFMA figure")
+    ap.add_argument("--no-batch64", action="store_true", help="skip the batch-16 and batch-64 MFMA figures")
     ap.add_argument("--weight-copies", type=int, default=None,
                     help="distinct weight copies the steps rotate over (default: >= 1 GB of "
                          "packed bits, beyond the 256 MB MALL; 1 keeps a block resident in it)")
@@ -326,40 +364,11 @@ def main():
     achieved = dom_bytes / (dom_us * 1e-6) / 1e9
     log(f"[bench] {sec * 1e6:.2f} us/block, {gbs:.1f} GB/s; groups {us_group}")
 
-    batch64 = None
+    batched = {}
     if not args.no_batch64 and B == 1:
-        log("[bench] block batch 64")
-        s64, g64, _, _ = run_block(te, torch, dev, LAYERS, GROUPS, 64, K, V,
-                                   max(20, args.steps // 10), max(3, args.warmup // 5),
-                                   per_launch=True)
-        fl = block_flops(LAYERS, 64)
-        dom_fl = 2 * 64 * 2 * 12288 * 4096
-        dom_tf = dom_fl / (g64[DOMINANT] * 1e-6) / 1e12
-        batch64 = {"us_per_block": round(s64 * 1e6, 2),
-                   "tflops": round(fl / s64 / 1e12, 2),
-                   "mfma_frac_of_fp16_peak": round(fl / s64 / 1e12 / MFMA_FP16_PEAK_TFLOPS, 4),
-                   "us_per_group_launch": g64,
-                   "roofline": {"bound": "mfma", "achieved": round(dom_tf, 2),
-                                "peak": MFMA_FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                                "frac": round(dom_tf / MFMA_FP16_PEAK_TFLOPS, 4),
-                                "kernel": "bgemm_kernel<K=3,MCG,V=1,NC=4> (+xfold, bfold) on "
-                                          "gate+up at batch 64",
-                                "avg_launch_us": g64[DOMINANT],
-                                "algorithmic_flops_per_launch": dom_fl}}
-        log(f"[bench] batch 64: {batch64['us_per_block']} us/block, {batch64['tflops']} TFLOP/s")
-        # the same block with the fp16-weight MFMA mode (each codebook value rounded once
-        # to fp16, one MAC per weight; max rel err ~2-3e-4 against the exact default)
-        s64h, g64h, _, _ = run_block(te, torch, dev, LAYERS, GROUPS, 64, K, V,
-                                     max(20, args.steps // 10), max(3, args.warmup // 5),
-                                     per_launch=True, mma_f16=True)
-        dom_tfh = dom_fl / (g64h[DOMINANT] * 1e-6) / 1e12
-        batch64["mma_f16"] = {"us_per_block": round(s64h * 1e6, 2),
-                              "tflops": round(fl / s64h / 1e12, 2),
-                              "mfma_frac_of_fp16_peak": round(fl / s64h / 1e12 / MFMA_FP16_PEAK_TFLOPS, 4),
-                              "us_per_group_launch": g64h,
-                              "gate_up_tflops": round(dom_tfh, 2)}
-        log(f"[bench] batch 64 mma_f16: {batch64['mma_f16']['us_per_block']} us/block, "
-            f"{batch64['mma_f16']['tflops']} TFLOP/s")
+        for bs in (16, 64):
+            batched[bs] = batched_figure(te, torch, dev, bs, K, V, args)
+    batch64 = batched.get(64)
 
     sweep = None
     if args.sweep:
@@ -427,6 +436,7 @@ def main():
                    "launches_per_block": [g for g, _ in GROUPS],
                    "us_per_group_launch": us_group,
                    "us_per_layer_single_launch": us_layer,
+                   "batch16": batched.get(16),
                    "batch64": batch64,
                    "sweep_configs4": sweep,
                    "next_rows": extra},

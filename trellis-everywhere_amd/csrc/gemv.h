@@ -312,20 +312,28 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
     for (int n = 0; n < NB; ++n) {
       t0[n] = 0.f;
       t1[n] = 0.f;
-      if (n >= nbv) continue;
-      for (int s0 = 0; s0 < m.S; s0 += 8) {
-        float q0[8], q1[8];
+    }
+    // up to 8 slices of every batch row in flight together: these loads miss the L2 (the
+    // partials come from other XCDs), so one round trip per 8 slices, not one per row
+    for (int s0 = 0; s0 < m.S; s0 += 8) {
+      float q0[NB][8], q1[NB][8];
+#pragma unroll
+      for (int n = 0; n < NB; ++n) {
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-          const float* p = obpart + (static_cast<size_t>(min(s0 + u, m.S - 1)) * NB + n) * 128;
-          q0[u] = __hip_atomic_load(p + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          q1[u] = __hip_atomic_load(p + lane + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          // rows past the call's repeat its last one (their sums are never stored)
+          const float* p = obpart + (static_cast<size_t>(min(s0 + u, m.S - 1)) * NB + min(n, nbv - 1)) * 128;
+          q0[n][u] = __hip_atomic_load(p + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          q1[n][u] = __hip_atomic_load(p + lane + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
+      }
+#pragma unroll
+      for (int n = 0; n < NB; ++n) {
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
           if (s0 + u < m.S) {
-            t0[n] += q0[u];
-            t1[n] += q1[u];
+            t0[n] += q0[n][u];
+            t1[n] += q1[n][u];
           }
         }
       }
