@@ -47,6 +47,7 @@ __device__ __forceinline__ void bg_out_fold(const LinArgs& g, const LinMat& m, c
     const int row = ob * 128 + min(lane + 64 * h, rows - 1);
     so[h] = m.sv[row] * m.osc[row] * nrm;
   }
+  const FwhtLane fl = fwht_lane(lane, m.block_out);
   for (int b = wave; b < nbv; b += WAVES) {
     float lo = tl[b * TLS + lane], hi = tl[b * TLS + lane + 64];
     if (NR == 2) {
@@ -59,7 +60,7 @@ __device__ __forceinline__ void bg_out_fold(const LinArgs& g, const LinMat& m, c
       lo = lo / 147.800537109375f;
       hi = hi / 147.800537109375f;
     }
-    fwht_chunk(lo, hi, m.block_out, lane);
+    fwht_chunk(lo, hi, m.block_out, lane, fl);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int rl = lane + 64 * h;

@@ -83,10 +83,10 @@ __device__ __forceinline__ float act_value(uint32_t w, long long i, int is_f16) 
 }
 
 // The value lane ^ H holds, without LDS: DPP for partners inside a 16-lane row
-// (quad_perm for 1 and 2; row rotations for 4 and 8, where row_ror:N hands lane i the value
-// of lane i - N within its row) and gfx950's permlane swaps for 16 and 32 (with both
-// operands equal, the first result holds the partner of the odd rows / upper half, the
-// second that of the even rows / lower half).
+// (quad_perm for 1 and 2; for 4, a quad reversal (lane j takes j ^ 3) followed by
+// row_half_mirror (lane i takes i ^ 7): (i ^ 7) ^ 3 = i ^ 4; row_ror:8 for 8) and gfx950's
+// permlane swaps for 16 and 32 (with both operands equal, the first result holds the
+// partner of the odd rows / upper half, the second that of the even rows / lower half).
 template <int H>
 __device__ __forceinline__ float lane_xor(float v, int lane) {
   const int iv = __builtin_bit_cast(int, v);
@@ -96,9 +96,8 @@ __device__ __forceinline__ float lane_xor(float v, int lane) {
   } else if constexpr (H == 2) {
     r = __builtin_amdgcn_mov_dpp(iv, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
   } else if constexpr (H == 4) {
-    const int dn = __builtin_amdgcn_mov_dpp(iv, 0x124, 0xF, 0xF, false);  // lane i - 4
-    const int up = __builtin_amdgcn_mov_dpp(iv, 0x12C, 0xF, 0xF, false);  // lane i + 4
-    r = (lane & 4) ? dn : up;
+    const int rev = __builtin_amdgcn_mov_dpp(iv, 0x1B, 0xF, 0xF, false);  // quad_perm [3,2,1,0]
+    r = __builtin_amdgcn_mov_dpp(rev, 0x141, 0xF, 0xF, false);            // row_half_mirror
   } else if constexpr (H == 8) {
     r = __builtin_amdgcn_mov_dpp(iv, 0x128, 0xF, 0xF, false);  // row_ror:8 = lane i ^ 8
   } else if constexpr (H == 16) {
@@ -112,30 +111,89 @@ __device__ __forceinline__ float lane_xor(float v, int lane) {
   return __builtin_bit_cast(float, r);
 }
 
+// One butterfly level (partner distance H <= 8) on values kept with a per-lane sign: a lane
+// stores st(l) = a(l) * v(l), a(l) = +-1, and the level computes st(l) + s(l) * st(l ^ H)
+// with s(l) = -1 where bit H of the lane is set. As a(l ^ H) = a(l) (no earlier level
+// touched bit H), that is a(l) * (v(l) + v(l ^ H)) in the lower lane and
+// -a(l) * (v(l ^ H) - v(l)) in the upper one: the Hadamard butterfly, each result rounded
+// once exactly as the plain add or subtract rounds it, with s(l) joining a(l). One DPP move
+// and one fma per value, in place of an add, a subtract and a select.
 template <int H>
-__device__ __forceinline__ void butterfly(float& lo, float& hi, int lane) {
-  const float plo = lane_xor<H>(lo, lane);
-  const float phi = lane_xor<H>(hi, lane);
-  const bool upper = (lane & H) != 0;
-  lo = upper ? plo - lo : lo + plo;
-  hi = upper ? phi - hi : hi + phi;
+__device__ __forceinline__ void butterfly(float& lo, float& hi, float s, int lane) {
+  lo = __builtin_fmaf(lane_xor<H>(lo, lane), s, lo);
+  hi = __builtin_fmaf(lane_xor<H>(hi, lane), s, hi);
+}
+
+// Butterfly levels 16 and 32 on both values at once: one permlane swap of (lo, hi) puts a
+// butterfly pair in every lane (lanes of the lower row / half: lo's pair (l, l + H); of the
+// upper: hi's pair (l - H, l)), the lane forms (lower + upper, lower - upper), and a second
+// swap puts the results back in place. Signs are unchanged (both values of a pair carry
+// the same a(l)).
+template <int H>
+__device__ __forceinline__ void butterfly_swap(float& lo, float& hi) {
+  uint32_t a, b;
+  if constexpr (H == 16) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, lo),
+                                                    __builtin_bit_cast(uint32_t, hi), false, false);
+    a = p[0];
+    b = p[1];
+  } else {
+    static_assert(H == 32, "partner distance");
+    const auto p = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, lo),
+                                                    __builtin_bit_cast(uint32_t, hi), false, false);
+    a = p[0];
+    b = p[1];
+  }
+  const float x = __builtin_bit_cast(float, a), y = __builtin_bit_cast(float, b);
+  const uint32_t sum = __builtin_bit_cast(uint32_t, x + y), dif = __builtin_bit_cast(uint32_t, x - y);
+  if constexpr (H == 16) {
+    const auto q = __builtin_amdgcn_permlane16_swap(sum, dif, false, false);
+    lo = __builtin_bit_cast(float, static_cast<uint32_t>(q[0]));
+    hi = __builtin_bit_cast(float, static_cast<uint32_t>(q[1]));
+  } else {
+    const auto q = __builtin_amdgcn_permlane32_swap(sum, dif, false, false);
+    lo = __builtin_bit_cast(float, static_cast<uint32_t>(q[0]));
+    hi = __builtin_bit_cast(float, static_cast<uint32_t>(q[1]));
+  }
+}
+
+// Per-lane constants of fwht_chunk for one block size: the signs s(l) of the levels 1 to 8
+// and the sign bit that restores a(l) at the end (computed once, used for many chunks).
+struct FwhtLane {
+  float s1, s2, s4, s8;
+  uint32_t flip;
+};
+
+__device__ __forceinline__ FwhtLane fwht_lane(int lane, int B) {
+  auto sgn = [&](int h) { return __builtin_bit_cast(float, 0x3F800000u | (static_cast<uint32_t>(lane & h) != 0u ? 0x80000000u : 0u)); };
+  return {sgn(1), sgn(2), sgn(4), sgn(8),
+          static_cast<uint32_t>(__builtin_popcount(lane & ((B < 16 ? B : 16) - 1)) & 1) << 31};
 }
 
 // Butterflies of a normalized-free block Hadamard (block B <= 128, a power of 2) on a
 // 128-element chunk held as lo = e[lane], hi = e[lane + 64]; pairs are exchanged in
-// registers (lane_xor), so a level costs a few VALU operations, not an LDS round trip.
-__device__ __forceinline__ void fwht_chunk(float& lo, float& hi, int B, int lane) {
-  if (B > 1) butterfly<1>(lo, hi, lane);
-  if (B > 2) butterfly<2>(lo, hi, lane);
-  if (B > 4) butterfly<4>(lo, hi, lane);
-  if (B > 8) butterfly<8>(lo, hi, lane);
-  if (B > 16) butterfly<16>(lo, hi, lane);
-  if (B > 32) butterfly<32>(lo, hi, lane);
+// registers (DPP, permlane swaps), so a level costs a few VALU operations, not an LDS
+// round trip. The levels 1 to 8 leave each lane's values multiplied by
+// a(l) = (-1)^popcount(l & (min(B, 16) - 1)) (butterfly); one sign flip at the end
+// restores them exactly. `fl` is fwht_lane(lane, B).
+__device__ __forceinline__ void fwht_chunk(float& lo, float& hi, int B, int lane, const FwhtLane& fl) {
+  if (B > 1) butterfly<1>(lo, hi, fl.s1, lane);
+  if (B > 2) butterfly<2>(lo, hi, fl.s2, lane);
+  if (B > 4) butterfly<4>(lo, hi, fl.s4, lane);
+  if (B > 8) butterfly<8>(lo, hi, fl.s8, lane);
+  if (B > 16) butterfly_swap<16>(lo, hi);
+  if (B > 32) butterfly_swap<32>(lo, hi);
   if (B == 128) {
     const float a = lo, b = hi;
     lo = a + b;
     hi = a - b;
   }
+  lo = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, lo) ^ fl.flip);
+  hi = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, hi) ^ fl.flip);
+}
+
+__device__ __forceinline__ void fwht_chunk(float& lo, float& hi, int B, int lane) {
+  fwht_chunk(lo, hi, B, lane, fwht_lane(lane, B));
 }
 
 __device__ __forceinline__ uint32_t dup_half(float v) {
@@ -203,13 +261,14 @@ __global__ __launch_bounds__(256) void xfold_kernel(LinArgs g) {
     w1[r] = __builtin_amdgcn_raw_buffer_load_b32(r_x, static_cast<int>(((row + e1) << xsh) & ~3u), 0, 0);
   }
   const float nrm = m.nrm_in;
+  const FwhtLane fl = fwht_lane(lane, m.block_in);
 #pragma unroll
   for (int r = 0; r < XFOLD_ROWS; ++r) {
     if (b0 + r >= g.batch) break;
     // an f16 row stride is even, so the element's half within its word follows e
     float lo = lane < kvalid ? act_value(w0[r], e0, g.x_f16) * s0 : 0.0f;
     float hi = lane + 64 < kvalid ? act_value(w1[r], e1, g.x_f16) * s1 : 0.0f;
-    fwht_chunk(lo, hi, m.block_in, lane);
+    fwht_chunk(lo, hi, m.block_in, lane, fl);
     if (g.mma_f16) {
       // fp16 values in tile-pair order (xf_pair_slot); columns k .. kp - 1 of the last
       // pair are written as zeros (lo and hi are zero there)

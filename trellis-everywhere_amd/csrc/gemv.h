@@ -146,6 +146,7 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
   // ---- activation fold: xf = Hb_k(isc_scaled * su * x) / sqrt(block_in) as (x,x) pairs
   {
     const float nrm = m.nrm_in;
+    const FwhtLane fl = fwht_lane(lane, m.block_in);
 #pragma unroll
     for (int f = 0; f < FCH; ++f) {
       const int ch = wave + GEMV_WAVES * f;
@@ -157,7 +158,7 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
         for (int n = 0; n < NB; ++n) {
           float lo = act_value(fw[f][n][0], e0, g.x_f16) * (fsu[f][0] * fis[f][0]);
           float hi = act_value(fw[f][n][1], e1, g.x_f16) * (fsu[f][1] * fis[f][1]);
-          fwht_chunk(lo, hi, m.block_in, lane);
+          fwht_chunk(lo, hi, m.block_in, lane, fl);
           xs[n * XROW + e0] = dup_half(lo * nrm);
           xs[n * XROW + e1] = dup_half(hi * nrm);
         }
@@ -341,6 +342,7 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
     if (lane == 0) __hip_atomic_store(m.tickets + ob, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   const float nrm = m.nrm_out;
+  const FwhtLane fl = fwht_lane(lane, m.block_out);
 #pragma unroll
   for (int n = 0; n < NB; ++n) {
     if (n >= nbv) break;
@@ -349,7 +351,7 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
       a = a / 147.800537109375f;
       b = b / 147.800537109375f;
     }
-    fwht_chunk(a, b, m.block_out, lane);
+    fwht_chunk(a, b, m.block_out, lane, fl);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int rl = lane + 64 * h;
