@@ -334,7 +334,8 @@ def main():
                     help="distinct weight copies the steps rotate over (default: >= 1 GB of "
                          "packed bits, beyond the 256 MB MALL; 1 keeps a block resident in it)")
     ap.add_argument("--mma-f16", action="store_true",
-                    help="batch >= 5: the fp16-weight MFMA mode (TRELLIS_MMA_F16) for the block run")
+                    help="the fp16-weight MFMA mode (TRELLIS_MMA_F16) for the block run (calls "
+                         "on the batched path)")
     ap.add_argument("--sweep", action="store_true", help="add the K x V sweep on the gate/up/down shapes")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
@@ -395,9 +396,9 @@ def main():
     if not args.no_extras and B == 1:
         log("[bench] extras: LM head (K=4) and embedding rows")
         extra = extras(te, torch, dev, max(40, args.steps // 5))
-        # small decode batches (the decode-GEMV carries up to 4 rows in its MFMA columns)
+        # small decode batches (the decode-GEMV carries the rows in its MFMA columns)
         small = {}
-        for bs in (2, 4):
+        for bs in (2, 4, 8):
             ssec_b, _, _, _ = run_block(te, torch, dev, LAYERS, GROUPS, bs, K, V,
                                         max(20, args.steps // 5), max(3, args.warmup // 5),
                                         per_launch=False)

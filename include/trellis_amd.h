@@ -60,8 +60,8 @@ typedef enum trellis_status {
 
 /* Flags of trellis_packed_linear_ex / trellis_packed_linear_group_ex. */
 enum trellis_flags {
-  /* The batched MFMA kernel only (batch >= 5; batch 1 to 4 run the exact decode-GEMV and
-   * ignore it): round each decoded codebook value once to fp16
+  /* The batched MFMA kernel only (calls that run the exact decode-GEMV, batch 1 to 4 and
+   * narrow groups at 5 to 16, ignore it): round each decoded codebook value once to fp16
    * (hi + lo in one fp16 add, i.e. the reference's exact fp32 sum, qtip.py:28-29, rounded
    * to nearest) and multiply it by the fp16 activation once, instead of the exact (hi, lo)
    * pair against a duplicated activation: half the MFMAs and half the activation bytes of
@@ -104,7 +104,8 @@ int trellis_workspace_bytes(const trellis_desc *W, int batch, size_t *bytes);
  *   x: [batch, k_in] with row stride ldx elements, dtype x_dtype (f16 or f32)
  *   y: [batch, n_out] with row stride ldy elements, dtype y_dtype (f16 or f32)
  * Batch 1 to 4 runs one decode-GEMV launch (gemv_kernel, x fold fused; the batch rows
- * ride the MFMA's columns). Larger batches run the x fold once (xfold_kernel), then the
+ * ride the MFMA's columns), and so does batch 5 to 16 when that launch's work items fit one
+ * round on the CUs. Other calls run the x fold once (xfold_kernel), then the
  * decode-once batched kernel (bgemm_kernel: each weight tile decoded once per 128 batch
  * columns and fed to exact fp16 MFMAs), and, when the launch plan splits k, the slice
  * reduction and output fold (bfold_kernel). */

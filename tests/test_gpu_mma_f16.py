@@ -8,7 +8,8 @@ multiplies it by the fp16 activation once. Bars:
     numpy's round-to-nearest-even cast, the folded activations rounded to fp16 as the
     kernels store them, float64 sums): <= 1e-4, far below the ~2e-4 the rounding itself
     moves the result, so a wrong pairing of tiles, halves or activations fails;
-  * batch 1 to 4 (the exact decode-GEMV) ignore the flag (bit-identical to the default call).
+  * calls that run the exact decode-GEMV (batch 1 to 4, and 5 to 16 for narrow groups)
+    ignore the flag (bit-identical to the default call).
 """
 import functools
 import sys
@@ -129,8 +130,10 @@ def test_mma_f16_dtypes(te, gpu_device):
     assert tn.rel_err(y16, x.astype(np.float64) @ W.T) < 2e-3
 
 
-@pytest.mark.parametrize("batch", [1, 3])
+@pytest.mark.parametrize("batch", [1, 3, 8])
 def test_mma_f16_ignored_by_the_gemv(te, gpu_device, batch):
+    """Calls that run the exact decode-GEMV (batch 1 to 4; batch 8 of this narrow matrix,
+    whose work items fit one round on the CUs) ignore the flag."""
     bits, rec, zq, W = _case(576, 1536, 3, "mcg", 1)
     lin = make_linear(te, bits, rec, gpu_device)
     x = torch.from_numpy(np.random.default_rng(1).standard_normal((batch, 1536)).astype(np.float16))

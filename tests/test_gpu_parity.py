@@ -319,3 +319,45 @@ def test_small_batch_group_strided(te, gpu_device):
     grp([xt] * 3, outs)
     for o, (_, _, W) in zip(outs, cases):
         assert tn.rel_err(o.float().cpu().numpy(), xs[:, :1024].astype(np.float64) @ W.T) < 2e-3
+
+
+@pytest.mark.parametrize("n,k,K,cb,V", [(1536, 576, 3, "3inst", 1), (576, 1536, 3, "mcg", 1),
+                                        (2048, 6144, 3, "mcg", 1), (208, 336, 3, "1mad", 1),
+                                        (384, 1024, 2, "3inst", 2), (96, 48, 4, "mcg", 1)])
+@pytest.mark.parametrize("batch", [5, 8, 9, 16])
+def test_batch_5_to_16_both_paths(te, gpu_device, monkeypatch, n, k, K, cb, V, batch):
+    """Batch 5 to 16 run the decode-GEMV (8 or 16 rows in the MFMA's B columns, shorter
+    k-ranges, one epilogue wave per row) or the batched path, as the planner decides
+    (TRELLIS_SMALL_BATCH_GEMV forces either): both within 1e-3 of the oracle, and within
+    fp32 summation order of each other."""
+    _say(f"[batch 5-16] n={n} k={k} K={K} cb={cb} V={V} batch={batch}")
+    bits, rec = tn.synthetic_record(n, k, K, seed=n + k + V, codebook=cb, V=V)
+    W = tn.w_hat_from_record(bits, rec)
+    lin = make_linear(te, bits, rec, gpu_device)
+    x = np.random.default_rng(batch + n).standard_normal((batch, k)).astype(np.float16)
+    xt = torch.from_numpy(x).to(gpu_device)
+    ref = x.astype(np.float64) @ W.T
+    ys = {}
+    for mode in ("1", "0"):
+        monkeypatch.setenv("TRELLIS_SMALL_BATCH_GEMV", mode)
+        ys[mode] = lin(xt).cpu().numpy()
+        assert tn.rel_err(ys[mode], ref) < TOL, mode
+        assert np.array_equal(ys[mode], lin(xt).cpu().numpy())     # deterministic
+    assert tn.rel_err(ys["1"], ys["0"]) < 1e-5
+
+
+def test_batch_5_to_16_group_strided(te, gpu_device, monkeypatch):
+    """A q/k/v-like group at batch 12 through the decode-GEMV (16 rows in the B columns,
+    split k) with strided f32 inputs and f16 outputs."""
+    monkeypatch.setenv("TRELLIS_SMALL_BATCH_GEMV", "1")
+    shapes = [(512, 2048), (128, 2048), (384, 2048)]
+    cases = [_record_and_w_hat(nn, kk, 3, "mcg") for nn, kk in shapes]
+    lins = [make_linear(te, b, r, gpu_device) for b, r, _ in cases]
+    grp = te.PackedGroup(lins)
+    xs = np.random.default_rng(12).standard_normal((12, 2048 + 64)).astype(np.float32)
+    xt = torch.from_numpy(xs).to(gpu_device)[:, :2048]
+    outs = [torch.zeros((12, nn + 32), dtype=torch.float16, device=gpu_device)[:, :nn]
+            for nn, _ in shapes]
+    grp([xt] * 3, outs)
+    for o, (_, _, W) in zip(outs, cases):
+        assert tn.rel_err(o.float().cpu().numpy(), xs[:, :2048].astype(np.float64) @ W.T) < 2e-3

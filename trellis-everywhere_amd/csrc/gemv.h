@@ -1,10 +1,12 @@
-// gemv.h — packed linear for batch 1 to 4 on gfx950: a pipelined decode-GEMV.
+// gemv.h — packed linear for batch 1 to 16 on gfx950: a pipelined decode-GEMV.
 //
 // The decode goes straight into the A operand of v_mfma_f32_16x16x32_f16 (the codebook's
 // fp16 pair (hi, lo) against a duplicated activation, fp32 accumulation: common.h),
 // organised for batch 1, where the decode's VALU work and fixed per-launch latencies, not
-// HBM, set the time. The MFMA's 16 B columns carry NB <= 4 batch rows (column n = batch
-// row n; NB = 1 at batch 1), so a few rows cost about what one does:
+// HBM, set the time. The MFMA's 16 B columns carry NB <= 16 batch rows (column n = batch
+// row n; NB = 1 at batch 1), so a few rows cost about what one does (the planner sends
+// batch 5 to 16 here only when the group's items fit one round on the CUs at the shorter
+// k-ranges that NB > 4 rows of folded activations in LDS allow):
 //
 //   * Work item = one matrix x one 128-row output block (8 bands of 16 rows) x one
 //     k-range of `kr` tile columns, run by one 16-wave workgroup (one per CU): waves w and
@@ -21,7 +23,8 @@
 //   * The two k-halves are added in LDS. With one k-range (S == 1) wave 0 applies
 //     y = sv * osc * Hb_n(t) directly; with split-K it publishes the block's partial sum,
 //     takes a ticket, and the last workgroup of the block adds the partials in slice order
-//     (deterministic) before the fold. sv * osc is loaded at kernel start.
+//     (deterministic) before the fold. Above 4 rows wave n does this for batch row n.
+//     sv * osc is loaded at kernel start.
 #pragma once
 
 #include "common.h"
@@ -30,6 +33,9 @@ namespace trellis {
 
 constexpr int GEMV_WAVES = 16;    // two waves per 16-row band: 128 rows per workgroup
 constexpr int GEMV_MAX_KR = 256;  // tile columns per k-range (4096 activations)
+// tile columns per k-range with NB batch rows: the rows' folded activations of one k-range
+// live in LDS as (x, x) pairs, 64 bytes per tile column and row
+__host__ __device__ constexpr int gemv_kr_max(int nb) { return nb <= 4 ? GEMV_MAX_KR : nb <= 8 ? 128 : 64; }
 constexpr int GEMV_PF = 2;        // pipeline stages in flight per wave
 constexpr int GEMV_G = 4;         // tiles decoded before their MFMAs are issued
 
@@ -41,17 +47,20 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
   constexpr int LOADS = (CH + 63) / 64;      // chunks per lane
   constexpr int CPT = NWK / 4;               // chunks per tile
   constexpr int SWP = LOADS * 256;           // words per wave buffer: every lane's chunks
-  constexpr int FCH = GEMV_MAX_KR * 16 / 128 / GEMV_WAVES;  // fold chunks per wave (max)
+  constexpr int KRM = gemv_kr_max(NB);       // tile columns per k-range (max)
+  constexpr int FCH = (KRM * 16 / 128 + GEMV_WAVES - 1) / GEMV_WAVES;  // fold chunks per wave
   // folded activations of the NB batch rows, rows 8 mod 64 words apart (bank spread)
-  constexpr int XROW = NB > 1 ? GEMV_MAX_KR * 16 + 8 : GEMV_MAX_KR * 16;
+  constexpr int XROW = NB > 1 ? KRM * 16 + 8 : KRM * 16;
+  static_assert(NB <= GEMV_WAVES, "one wave per batch row in the epilogue");
   __shared__ __align__(16) uint32_t stg[GEMV_WAVES * SWP];
   __shared__ __align__(16) uint32_t xs[NB * XROW];
   __shared__ float tt[2][NB][128];
-  __shared__ unsigned ready[GEMV_MAX_KR / 8];   // per 128-column chunk of xs: rows folded
-  __shared__ unsigned nready;                    // chunks folded so far
+  __shared__ unsigned ready[KRM / 8];   // per 128-column chunk of xs: rows folded
+  __shared__ unsigned nready;           // chunks folded so far
+  __shared__ unsigned ticket_sh;        // split-K ticket, shared with every wave (NB > 4)
   // the wave index is uniform: kept scalar, so per-wave choices are scalar branches
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  if (threadIdx.x < GEMV_MAX_KR / 8) ready[threadIdx.x] = 0u;
+  if (threadIdx.x < KRM / 8) ready[threadIdx.x] = 0u;
   if (threadIdx.x == 0) nready = 0u;
   __syncthreads();
   const int bl = wave & 7, half = wave >> 3;     // band of the block, half of the k-range
@@ -156,6 +165,7 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
         // element's half within its word follows e
 #pragma unroll
         for (int n = 0; n < NB; ++n) {
+          if (n >= nbv) break;               // rows past the call's are never read
           float lo = act_value(fw[f][n][0], e0, g.x_f16) * (fsu[f][0] * fis[f][0]);
           float hi = act_value(fw[f][n][1], e1, g.x_f16) * (fsu[f][1] * fis[f][1]);
           fwht_chunk(lo, hi, m.block_in, lane, fl);
@@ -281,6 +291,79 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
     for (int i = 0; i < 4; ++i) tt[half][r][bl * 16 + 4 * gq + i] = acc[i];
   }
   __syncthreads();
+  if constexpr (NB > 4) {
+    // ---- wave n finishes batch row n: the two k-halves, then (split-K) every row's
+    // partial sum published, one ticket per workgroup, and in the last workgroup of the
+    // block each wave adds its row's partials in slice order; then y = sv * osc * Hb_n(t)
+    const int n = wave;
+    const bool mine = n < nbv;
+    float t0 = 0.f, t1 = 0.f;
+    if (mine) {
+      t0 = tt[0][n][lane] + tt[1][n][lane];
+      t1 = tt[0][n][lane + 64] + tt[1][n][lane + 64];
+    }
+    if (m.S > 1) {
+      // partial sums [block][slice][NB][128]
+      float* mypart = m.part + (static_cast<size_t>(ob) * m.S + sl) * NB * 128 + n * 128;
+      if (mine) {
+        __hip_atomic_store(mypart + lane, t0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(mypart + lane + 64, t1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();   // every row's partial sum is stored before the ticket is taken
+      if (wave == 0) {
+        unsigned prev = 0;
+        if (lane == 0)
+          prev = __hip_atomic_fetch_add(m.tickets + ob, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        prev = __builtin_amdgcn_readfirstlane(prev);
+        if (lane == 0) ticket_sh = prev;
+      }
+      __syncthreads();
+      if (ticket_sh != static_cast<unsigned>(m.S - 1)) return;
+      if (wave == 0 && lane == 0)
+        __hip_atomic_store(m.tickets + ob, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (!mine) return;
+      const float* rowpart = m.part + static_cast<size_t>(ob) * m.S * NB * 128 + n * 128;
+      t0 = 0.f;
+      t1 = 0.f;
+      for (int s0 = 0; s0 < m.S; s0 += 8) {
+        float q0[8], q1[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const float* p = rowpart + static_cast<size_t>(min(s0 + u, m.S - 1)) * NB * 128;
+          q0[u] = __hip_atomic_load(p + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          q1[u] = __hip_atomic_load(p + lane + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (s0 + u < m.S) {
+            t0 += q0[u];
+            t1 += q1[u];
+          }
+        }
+      }
+    }
+    if (!mine) return;
+    if (CB == CB_1MAD) {
+      t0 = t0 / 147.800537109375f;
+      t1 = t1 / 147.800537109375f;
+    }
+    fwht_chunk(t0, t1, m.block_out, lane);
+    const float nrm = m.nrm_out;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int rl = lane + 64 * h;
+      if (rl < rows) {
+        const float v = (h ? t1 : t0) * nrm * so[h];
+        const long long o = n * m.ldy + ob * 128 + rl;
+        if (g.y_f16)
+          static_cast<_Float16*>(m.y)[o] = static_cast<_Float16>(v);
+        else
+          static_cast<float*>(m.y)[o] = v;
+      }
+    }
+    return;
+  }
   if (wave != 0) return;
 
   // ---- wave 0: the two k-halves, then (split-K) publish, ticket, and in the last

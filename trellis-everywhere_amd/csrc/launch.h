@@ -12,8 +12,10 @@
 namespace trellis {
 
 // gemv_kernel<K, cb, V, kc, nb> over g.total items (batch g.batch <= GEMV_MAX_NB, nb the
-// smallest of 1, 2, 4 that holds it; k-ranges of g.kr tiles).
-constexpr int GEMV_MAX_NB = 4;
+// smallest of 1, 2, 4, 8, 16 that holds it, gemv_nb; k-ranges of g.kr <= gemv_kr_max(nb)
+// tiles).
+constexpr int GEMV_MAX_NB = 16;
+constexpr int gemv_nb(int batch) { return batch <= 1 ? 1 : batch == 2 ? 2 : batch <= 4 ? 4 : batch <= 8 ? 8 : 16; }
 template <int K>
 int launch_gemv_k(int cb, int V, int kc, const LinArgs& g, hipStream_t st);
 
@@ -61,9 +63,13 @@ static int launch_gemv_nb(int kc, const LinArgs& g, hipStream_t st) {
 
 template <int K, int CB, int V>
 static int launch_gemv_kc(int kc, const LinArgs& g, hipStream_t st) {
-  if (g.batch <= 1) return launch_gemv_nb<K, CB, V, 1>(kc, g, st);
-  if (g.batch == 2) return launch_gemv_nb<K, CB, V, 2>(kc, g, st);
-  return launch_gemv_nb<K, CB, V, GEMV_MAX_NB>(kc, g, st);
+  switch (gemv_nb(g.batch)) {
+    case 1: return launch_gemv_nb<K, CB, V, 1>(kc, g, st);
+    case 2: return launch_gemv_nb<K, CB, V, 2>(kc, g, st);
+    case 4: return launch_gemv_nb<K, CB, V, 4>(kc, g, st);
+    case 8: return launch_gemv_nb<K, CB, V, 8>(kc, g, st);
+    default: return launch_gemv_nb<K, CB, V, 16>(kc, g, st);
+  }
 }
 
 template <int K, int CB>

@@ -1,6 +1,7 @@
 // trellis_amd.hip — C ABI (include/trellis_amd.h): validation, launch planning, the
 // bit-exact tile decode kernel and the dispatch to the decode-matmul kernels (gemv_kernel at
-// batch 1 to 4, xfold_kernel + bgemm_kernel (+ bfold_kernel) above).
+// batch 1 to 4 and, where use_gemv picks it, 5 to 16; xfold_kernel + bgemm_kernel
+// (+ bfold_kernel) otherwise).
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -102,19 +103,24 @@ int device_cus() {
   return cus;
 }
 
-// Batch 1 to 4 (gemv_kernel): a work item is one 128-row output block x one k-range of kr tile
-// columns (kr a multiple of 8, so a k-range holds whole 128-column fold chunks), run by one
-// 16-wave workgroup; one workgroup fits a CU. kr minimises an estimate of the launch time in
+// Batch 1 to 4, and 5 to 16 where the group is narrow (gemv_kernel): a work item is one
+// 128-row output block x one k-range of kr tile columns (kr a multiple of 8, so a k-range
+// holds whole 128-column fold chunks, and at most gemv_kr_max(nb)), run by one 16-wave
+// workgroup; one workgroup fits a CU. kr minimises an estimate of the launch time in
 // 2.4 GHz cycles: rounds of items over the CUs x the decode of 8 bands x kr/2 tiles per wave
-// at ~50 cycles per tile with four waves per SIMD, plus ~2 us of split-K epilogue (publish,
+// at ~50 cycles per tile with four waves per SIMD (above 4 rows, plus the fold of kr x 16
+// activations of every row in each workgroup), plus ~2 us of split-K epilogue (publish,
 // ticket, reduce) and ~0.1 us of ticket contention per slice when kr does not cover k, plus
 // a first-load latency for every round after the first. TRELLIS_GEMV_KR forces a value.
-int gemv_kr(const trellis_desc* const* W, int count) {
+int gemv_kr(const trellis_desc* const* W, int count, int batch) {
+  const int nb = gemv_nb(batch), krm = gemv_kr_max(nb);
   int maxt = 0;
   for (int i = 0; i < count; ++i) maxt = W[i]->k_in / 16 > maxt ? W[i]->k_in / 16 : maxt;
-  const int cap = ((maxt + 7) / 8) * 8 < GEMV_MAX_KR ? ((maxt + 7) / 8) * 8 : GEMV_MAX_KR;
+  const int cap = ((maxt + 7) / 8) * 8 < krm ? ((maxt + 7) / 8) * 8 : krm;
   const int forced = env_int("TRELLIS_GEMV_KR", 0);
-  if (forced >= 8 && forced <= GEMV_MAX_KR && forced % 8 == 0) return forced;
+  if (forced >= 8 && forced <= krm && forced % 8 == 0) return forced;
+  // the per-workgroup fold of every row (~2 model units per tile column and row)
+  const long long per_kr = 100 + (nb > 4 ? 2 * nb : 0);
   const long long cus = device_cus();
   int best = 8;
   long long best_cost = -1;
@@ -127,7 +133,7 @@ int gemv_kr(const trellis_desc* const* W, int count) {
       smax = S > smax ? S : smax;
     }
     const long long rounds = (items + cus - 1) / cus;
-    const long long cost = rounds * kr * 100 + (smax > 1 ? 4800 + 240 * smax : 0) +
+    const long long cost = rounds * kr * per_kr + (smax > 1 ? 4800 + 240 * smax : 0) +
                            (rounds - 1) * 3600;
     if (best_cost < 0 || cost < best_cost) {
       best = kr;
@@ -184,13 +190,33 @@ int bgemm_kr(const trellis_desc* const* W, int count, int batch, int nc, bool f1
   return best;
 }
 
+// The decode-GEMV for batch 1 to 4, and for 5 to 16 when its items at the longest k-range
+// (gemv_kr_max) fit one round on the CUs: every workgroup folds the activations of its
+// k-range for all rows, and the cap on the k-range that the rows' LDS imposes multiplies
+// the items of a long k or a wide group; otherwise the batched path, with its two extra
+// launches (x fold, split-K fold), is faster (measured on the 8B block: the gemv wins for
+// q/k/v and o at batch 5 to 16 and for down at 5 to 8, by 1.3-5 us per launch; gate+up
+// and down at 16 need two or more rounds and lose by 4-15 us). TRELLIS_SMALL_BATCH_GEMV
+// = 1 / 0 forces the choice for batch 5 to 16.
+bool use_gemv(const trellis_desc* const* W, int count, int batch) {
+  if (batch <= 4) return true;
+  if (batch > GEMV_MAX_NB) return false;
+  const int forced = env_int("TRELLIS_SMALL_BATCH_GEMV", -1);
+  if (forced == 0 || forced == 1) return forced == 1;
+  const int krm = gemv_kr_max(gemv_nb(batch));
+  long long items = 0;
+  for (int i = 0; i < count; ++i)
+    items += static_cast<long long>((W[i]->n_out + 127) / 128) * ((W[i]->k_in / 16 + krm - 1) / krm);
+  return items <= device_cus();
+}
+
 GroupPlan group_plan(const trellis_desc* const* W, int count, int batch, bool f16) {
   GroupPlan p;
-  p.gemv = batch <= GEMV_MAX_NB;
+  p.gemv = use_gemv(W, count, batch);
   p.nb = batch;
   p.nc = bgemm_nc(batch);
   p.ncb = p.gemv ? 1 : (batch + 16 * p.nc - 1) / (16 * p.nc);
-  p.kr = p.gemv ? gemv_kr(W, count) : bgemm_kr(W, count, batch, p.nc, f16);
+  p.kr = p.gemv ? gemv_kr(W, count, batch) : bgemm_kr(W, count, batch, p.nc, f16);
   p.kc = p.kr >= 32 ? 16 : 8;
   {
     const int kc = env_int("TRELLIS_GEMV_KC", 0);
@@ -199,8 +225,8 @@ GroupPlan group_plan(const trellis_desc* const* W, int count, int batch, bool f1
   p.total = 0;
   p.folds = 0;
   p.ws = 0;
-  // partial sums per (block, slice): the gemv's 1, 2 or 4 batch rows, or bgemm's 16 * NC
-  const int part_cols = p.gemv ? (batch == 1 ? 1 : batch == 2 ? 2 : GEMV_MAX_NB) : 16 * p.nc;
+  // partial sums per (block, slice): the gemv's NB batch rows, or bgemm's 16 * NC
+  const int part_cols = p.gemv ? gemv_nb(batch) : 16 * p.nc;
   for (int i = 0; i < count; ++i) {
     p.n_ob[i] = (W[i]->n_out + 127) / 128;
     p.S[i] = (W[i]->k_in / 16 + p.kr - 1) / p.kr;
@@ -221,7 +247,8 @@ GroupPlan group_plan(const trellis_desc* const* W, int count, int batch, bool f1
   return p;
 }
 
-// Batch 1 to 4: the pipelined decode-GEMV (its x fold is fused).
+// The pipelined decode-GEMV (its x fold is fused): batch 1 to 4, and 5 to 16 where
+// use_gemv picks it.
 int launch_gemv(int K, int cb, int V, int kc, const LinArgs& g, hipStream_t st) {
   switch (K) {
     case 2: return launch_gemv_k<2>(cb, V, kc, g, st);
@@ -230,7 +257,7 @@ int launch_gemv(int K, int cb, int V, int kc, const LinArgs& g, hipStream_t st) 
   }
 }
 
-// The x fold of every member (batch > 4), written once to the workspace.
+// The x fold of every member (the batched path), written once to the workspace.
 int launch_xfold(LinArgs& g, int folds, hipStream_t st) {
   const int items = g.total;
   g.total = folds;
@@ -465,7 +492,7 @@ int trellis_packed_linear_group_ex(const trellis_desc* const* W, int count, cons
   if (v) return v;
   if (flags & ~TRELLIS_MMA_F16) return TRELLIS_ERR_FLAGS;
   // the flag concerns the batched MFMA kernel only (the decode-GEMV is exact)
-  const bool f16 = (flags & TRELLIS_MMA_F16) != 0 && batch > GEMV_MAX_NB;
+  const bool f16 = (flags & TRELLIS_MMA_F16) != 0 && !use_gemv(W, count, batch);
   if (!x || !y || !ldx || !ldy) return TRELLIS_ERR_NULL;
   if (batch < 1) return TRELLIS_ERR_BATCH;
   if ((x_dtype != TRELLIS_F32 && x_dtype != TRELLIS_F16) ||

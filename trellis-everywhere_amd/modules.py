@@ -24,7 +24,7 @@ class TrellisLinear(torch.nn.Module):
 
     x: [..., in_features] (f16, f32 or bf16) on the linear's device. The output has x's
     dtype (bf16 is computed in fp32 and rounded once). mma_f16 selects the batched
-    kernel's fp16-weight mode (rows >= 5 only; see PackedLinear.forward)."""
+    kernel's fp16-weight mode (calls on the batched path only; see PackedLinear.forward)."""
 
     def __init__(self, packed: PackedLinear, bias: torch.Tensor | None = None,
                  mma_f16: bool = False):

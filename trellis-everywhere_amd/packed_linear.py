@@ -99,8 +99,9 @@ class PackedLinear:
                 workspace: torch.Tensor | None = None, mma_f16: bool = False) -> torch.Tensor:
         """y = W_hat @ x for x [k_in] or [batch, k_in] (fp16 or fp32, on this device).
 
-        mma_f16 (batch >= 5 only): round each codebook value once to fp16 and use one MAC
-        per weight in the batched kernel (TRELLIS_MMA_F16: ~2-3e-4 max rel err against the
+        mma_f16 (calls on the batched path only: batch > 16, or 5 to 16 for wide groups):
+        round each codebook value once to fp16 and use one MAC per weight in the batched
+        kernel (TRELLIS_MMA_F16: ~2-3e-4 max rel err against the
         exact default, about half the MFMA work and activation traffic)."""
         lib = _capi.load()
         squeeze = x.dim() == 1
