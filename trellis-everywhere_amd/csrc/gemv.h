@@ -35,7 +35,7 @@ constexpr int GEMV_WAVES = 16;    // two waves per 16-row band: 128 rows per wor
 constexpr int GEMV_MAX_KR = 256;  // tile columns per k-range (4096 activations)
 // tile columns per k-range with NB batch rows: the rows' folded activations of one k-range
 // live in LDS as (x, x) pairs, 64 bytes per tile column and row
-__host__ __device__ constexpr int gemv_kr_max(int nb) { return nb <= 4 ? GEMV_MAX_KR : nb <= 8 ? 128 : 64; }
+__host__ __device__ constexpr int gemv_kr_max(int nb) { return nb <= 4 ? GEMV_MAX_KR : nb <= 8 ? 128 : 96; }
 constexpr int GEMV_PF = 2;        // pipeline stages in flight per wave
 constexpr int GEMV_G = 4;         // tiles decoded before their MFMAs are issued
 

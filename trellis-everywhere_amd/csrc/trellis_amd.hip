@@ -195,8 +195,8 @@ int bgemm_kr(const trellis_desc* const* W, int count, int batch, int nc, bool f1
 // k-range for all rows, and the cap on the k-range that the rows' LDS imposes multiplies
 // the items of a long k or a wide group; otherwise the batched path, with its two extra
 // launches (x fold, split-K fold), is faster (measured on the 8B block: the gemv wins for
-// q/k/v and o at batch 5 to 16 and for down at 5 to 8, by 1.3-5 us per launch; gate+up
-// and down at 16 need two or more rounds and lose by 4-15 us). TRELLIS_SMALL_BATCH_GEMV
+// q/k/v, o and down at batch 5 to 16, by 1-5 us per launch; gate+up needs two or more
+// rounds and loses by 4-15 us). TRELLIS_SMALL_BATCH_GEMV
 // = 1 / 0 forces the choice for batch 5 to 16.
 bool use_gemv(const trellis_desc* const* W, int count, int batch) {
   if (batch <= 4) return true;
