@@ -1,8 +1,9 @@
 """The packed linear inside captured HIP graphs (what bench.py times): every replay, with new
 inputs copied in and eager calls of the same linears between the replays, must equal the
 eager call on the same inputs bit for bit. Covers the batch-1 split-K tickets (reset by the
-kernels, no memset in the graph), the batch 2-4 decode-GEMV, the batched path with its
-x-fold and split-K fold launches, and the fp16-weight mode."""
+kernels, no memset in the graph), the decode-GEMV with 4 and 16 rows in its MFMA columns
+(batch 3, 12; split k, one ticket per workgroup), the batched path with its x-fold and
+split-K fold launches, and the fp16-weight mode."""
 import sys
 
 import numpy as np
@@ -25,7 +26,8 @@ def make_linear(te, bits, rec, device):
     return te.PackedLinear(r, device=device)
 
 
-@pytest.mark.parametrize("batch,mma_f16", [(1, False), (3, False), (64, False), (64, True)])
+@pytest.mark.parametrize("batch,mma_f16", [(1, False), (3, False), (12, False), (64, False),
+                                           (64, True)])
 def test_graph_replays_match_eager(te, gpu_device, batch, mma_f16):
     _say(f"[graph] batch={batch} mma_f16={mma_f16}")
     shapes = [(1024, 2048), (256, 2048), (512, 2048)]      # split-K plans at every batch

@@ -151,8 +151,12 @@ int gemv_kr(const trellis_desc* const* W, int count, int batch) {
 // ~75 + NC x ~10)) plus, with split-K, the bfold_kernel
 // launch (~1.5 us) and the partial blocks it moves (S x rows x NB x 4 bytes written and
 // read at ~2.5 KB per cycle), plus a start-up latency per round after the first.
-// TRELLIS_BGEMM_KR forces a value.
-int bgemm_nc(int batch) { return batch <= 16 ? 1 : batch <= 32 ? 2 : batch <= 64 ? 4 : 8; }
+// TRELLIS_BGEMM_KR forces a value, TRELLIS_BGEMM_NC the column-block width.
+int bgemm_nc(int batch) {
+  const int forced = env_int("TRELLIS_BGEMM_NC", 0);
+  if (forced == 1 || forced == 2 || forced == 4 || forced == 8) return forced;
+  return batch <= 16 ? 1 : batch <= 32 ? 2 : batch <= 64 ? 4 : 8;
+}
 
 int bgemm_kr(const trellis_desc* const* W, int count, int batch, int nc, bool f16) {
   int maxt = 0;
