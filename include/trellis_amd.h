@@ -95,7 +95,9 @@ typedef struct trellis_desc {
 
 /* Number of workspace bytes trellis_packed_linear needs for this layer and batch.
  * The workspace must be zero-filled once when allocated; every call leaves its
- * counters at zero again. Replaces the per-call scratch f32buf allocations of
+ * counters at zero again. It belongs to one layer (or one group): its counters sit in a
+ * header laid out by the members' shapes alone, so calls at any batch size may share it
+ * (sized for the largest), but another layer's calls may not. Replaces the per-call scratch f32buf allocations of
  * web/packed.js:165-180. */
 int trellis_workspace_bytes(const trellis_desc *W, int batch, size_t *bytes);
 

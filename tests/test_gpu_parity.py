@@ -361,3 +361,18 @@ def test_batch_5_to_16_group_strided(te, gpu_device, monkeypatch):
     grp([xt] * 3, outs)
     for o, (_, _, W) in zip(outs, cases):
         assert tn.rel_err(o.float().cpu().numpy(), xs[:, :2048].astype(np.float64) @ W.T) < 2e-3
+
+
+def test_workspace_shared_across_batch_sizes(te, gpu_device):
+    """One linear's workspace serves calls at every batch size: a large batched call fills
+    it with partial sums and folded activations, and the split-K tickets of the calls after
+    it (decode-GEMV at 1, 3, 8; batched at 64) sit in a header that no call's data reaches,
+    so each result stays within 1e-3 of the oracle."""
+    bits, rec, W = _record_and_w_hat(2048, 6144, 3, "mcg")
+    lin = make_linear(te, bits, rec, gpu_device)
+    rng = np.random.default_rng(77)
+    for batch in (300, 1, 3, 8, 64, 1, 300, 2):
+        _say(f"[workspace] batch={batch}")
+        x = rng.standard_normal((batch, 6144)).astype(np.float16)
+        y = lin(torch.from_numpy(x).to(gpu_device)).cpu().numpy()
+        assert tn.rel_err(y, x.astype(np.float64) @ W.T) < TOL, batch

@@ -228,23 +228,27 @@ GroupPlan group_plan(const trellis_desc* const* W, int count, int batch, bool f1
   }
   p.total = 0;
   p.folds = 0;
+  // Workspace: a header of counters whose layout depends only on the members' shapes (one
+  // split-K ticket per 128-row block of every member); every call leaves them at zero.
+  // Plans for other batch sizes reuse the same workspace, so their data (partial sums,
+  // folded activations) only ever lies past the header, and a ticket never starts from
+  // another plan's data.
   p.ws = 0;
+  for (int i = 0; i < count; ++i) {
+    p.n_ob[i] = (W[i]->n_out + 127) / 128;
+    p.off_tickets[i] = p.ws;
+    p.ws += align256(static_cast<size_t>(p.n_ob[i]) * 4);
+  }
   // partial sums per (block, slice): the gemv's NB batch rows, or bgemm's 16 * NC
   const int part_cols = p.gemv ? gemv_nb(batch) : 16 * p.nc;
   for (int i = 0; i < count; ++i) {
-    p.n_ob[i] = (W[i]->n_out + 127) / 128;
     p.S[i] = (W[i]->k_in / 16 + p.kr - 1) / p.kr;
     p.total += p.n_ob[i] * p.ncb * p.S[i];
     p.folds += p.nb * ((W[i]->k_in + 127) / 128);
-    p.off_tickets[i] = p.ws;
-    if (p.S[i] > 1) {
-      p.ws += align256(static_cast<size_t>(p.n_ob[i]) * p.ncb * 4);
-      p.off_part[i] = p.ws;
+    p.off_part[i] = p.ws;
+    if (p.S[i] > 1)
       p.ws += align256(static_cast<size_t>(p.n_ob[i]) * p.ncb * p.S[i] * part_cols * 128 *
                        sizeof(float));
-    } else {
-      p.off_part[i] = p.ws;
-    }
     p.off_xf[i] = p.ws;
     if (!p.gemv) p.ws += align256(static_cast<size_t>(p.nb) * W[i]->k_in * 4);
   }
@@ -270,7 +274,7 @@ int launch_xfold(LinArgs& g, int folds, hipStream_t st) {
   return hipGetLastError() == hipSuccess ? TRELLIS_OK : TRELLIS_ERR_LAUNCH;
 }
 
-// Batch >= 2: the x fold, the decode-once batched kernel, and (split-K) its reduction.
+// The batched path: the x fold, the decode-once batched kernel, and (split-K) its reduction.
 int launch_bgemm(int K, int cb, int V, int nc, LinArgs& g, int folds, int nfold, hipStream_t st) {
   int v = launch_xfold(g, folds, st);
   if (v) return v;
