@@ -145,8 +145,8 @@ int gemv_kr(const trellis_desc* const* W, int count, int batch) {
 
 // Batch >= 2 (bgemm_kernel): NC 16-column batch chunks per workgroup (up to 128 columns),
 // a work item is one 128-row block x one column block x one k-range of kr tile columns
-// (a multiple of the k-step: 8 tiles up to 64 columns and in the fp16-weight mode, else
-// 4), run by one 16-wave workgroup per CU. kr minimises ceil(items/CUs) x the per-SIMD work
+// (a multiple of the k-step: 16 tiles at 16 columns, 8 up to 64 and in the fp16-weight
+// mode, else 4), run by one 16-wave workgroup per CU. kr minimises ceil(items/CUs) x the per-SIMD work
 // of an item (2 bands x kr tiles x (decode ~61 + NC MFMAs x ~19 cycles; fp16-weight mode
 // ~75 + NC x ~10)) plus, with split-K, the bfold_kernel
 // launch (~1.5 us) and the partial blocks it moves (S x rows x NB x 4 bytes written and
@@ -161,7 +161,7 @@ int bgemm_nc(int batch) {
 int bgemm_kr(const trellis_desc* const* W, int count, int batch, int nc, bool f16) {
   int maxt = 0;
   for (int i = 0; i < count; ++i) maxt = W[i]->k_in / 16 > maxt ? W[i]->k_in / 16 : maxt;
-  const int kt = (f16 || nc <= 4) ? 8 : 4;
+  const int kt = f16 ? 8 : nc == 1 ? 16 : nc <= 4 ? 8 : 4;   // BgStep<nc, f16>::KT
   // per band-tile SIMD cycles: the decode and NC MFMAs (the fp16-weight mode decodes a
   // little more and issues half the MFMAs)
   const long long tile_cost = f16 ? 75 + 10 * nc : 61 + 19 * nc;
