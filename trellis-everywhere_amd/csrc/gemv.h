@@ -108,19 +108,29 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
   // fold jobs: the k-range's 128-column chunks, chunk ch folded by wave ch % GEMV_WAVES
   // for every batch row (spreading the (chunk, row) pairs over all the waves measured
   // slower: every wave then folds before its first decode)
-  const int njobs = nch;
+  // With 16 rows (one chunk per wave at most) the rows of a chunk are split over
+  // wpc = 16 / nch waves, so few chunks of many rows still keep every wave folding: wave w
+  // folds rows [f_r0, f_r1) of chunk w % nch (8B block at batch 16: q/k/v and o launches
+  // ~0.5 us faster; at 8 rows it measured ~0.5 us slower, so 8 rows keep a chunk per wave).
+  constexpr bool SPLIT = NB > 8;
+  const int wpc = SPLIT ? max(1, GEMV_WAVES / nch) : 1;
+  const int f_rpw = (nbv + wpc - 1) / wpc;
+  const int f_r0 = SPLIT ? (wave / nch) * f_rpw : 0;
+  const int f_r1 = SPLIT ? min(nbv, f_r0 + f_rpw) : nbv;
+  const int f_ch0 = SPLIT ? (wave < nch * wpc ? wave % nch : nch) : wave;
+  const int njobs = SPLIT ? nch * nbv : nch;     // rows folded (SPLIT) or chunks
   uint32_t fw[FCH][NB][2];
   float fsu[FCH][2], fis[FCH][2];
 #pragma unroll
   for (int f = 0; f < FCH; ++f) {
-    const int ch = wave + GEMV_WAVES * f;
+    const int ch = f_ch0 + GEMV_WAVES * f;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const unsigned e = ch < nch ? ch * 128 + lane + 64 * h : RSRC_OOB / 4;
 #pragma unroll
       for (int n = 0; n < NB; ++n) {
-        // batch row n of the call (rows past it read zeros)
-        const unsigned en = n < nbv && ch < nch ? n * ldx + e : RSRC_OOB / 4;
+        // batch row n of the call (rows past it, or not this wave's, read zeros)
+        const unsigned en = n >= f_r0 && n < f_r1 && ch < nch ? n * ldx + e : RSRC_OOB / 4;
         fw[f][n][h] = __builtin_amdgcn_raw_buffer_load_b32(r_x, static_cast<int>(((en << xsh) & ~3u)), 0, 0);
       }
       fsu[f][h] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r_su, static_cast<int>(e * 4), 0, 0));
@@ -158,26 +168,28 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
     const FwhtLane fl = fwht_lane(lane, m.block_in);
 #pragma unroll
     for (int f = 0; f < FCH; ++f) {
-      const int ch = wave + GEMV_WAVES * f;
-      if (ch < nch) {
+      const int ch = f_ch0 + GEMV_WAVES * f;
+      if (ch < nch && f_r1 > f_r0) {
         const int e0 = ch * 128 + lane, e1 = e0 + 64;
         // columns past the k-range loaded as zeros; an f16 row stride is even, so the
         // element's half within its word follows e
 #pragma unroll
         for (int n = 0; n < NB; ++n) {
-          if (n >= nbv) break;               // rows past the call's are never read
+          if (n >= f_r1) break;              // rows past the call's are never read
+          if (n < f_r0) continue;
           float lo = act_value(fw[f][n][0], e0, g.x_f16) * (fsu[f][0] * fis[f][0]);
           float hi = act_value(fw[f][n][1], e1, g.x_f16) * (fsu[f][1] * fis[f][1]);
           fwht_chunk(lo, hi, m.block_in, lane, fl);
           xs[n * XROW + e0] = dup_half(lo * nrm);
           xs[n * XROW + e1] = dup_half(hi * nrm);
         }
-        // publish the chunk (all its rows): its xs words are written before the count
+        // publish the chunk's rows: their xs words are written before the count
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         if (lane == 0) {
-          __hip_atomic_fetch_add(&ready[ch], static_cast<unsigned>(nbv), __ATOMIC_RELAXED,
+          __hip_atomic_fetch_add(&ready[ch], static_cast<unsigned>(f_r1 - f_r0), __ATOMIC_RELAXED,
                                  __HIP_MEMORY_SCOPE_WORKGROUP);
-          __hip_atomic_fetch_add(&nready, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          __hip_atomic_fetch_add(&nready, SPLIT ? static_cast<unsigned>(f_r1 - f_r0) : 1u,
+                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
       }
     }
