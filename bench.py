@@ -14,8 +14,9 @@ n*k*K/8). The JSON line also carries us/layer, the dominant launch's HBM rooflin
 duration from HIP events on the launch stream), the same block at batch 16 and 64 with
 their fp16 MFMA rooflines (algorithmic 2*B*n*k flops), and a CPU baseline: this repo's torch-CPU
 restatement of the reference decode+restore+matmul (oracle/torch_cpu.py) on a bounded
-sample. --sweep adds the sweep K=2,3,4 x V=1,2 on the gate/up/down shapes at
-batch 1 and at a 512-token prefill.
+sample, per configuration and layer. The bit-rate sweep (configs[4]: K=2,3,4 x V=1,2 on
+the 8B gate/up/down shapes, at batch 1 and at a 512-token prefill) runs by default
+(--no-sweep skips it), each point with its own roofline.
 """
 from __future__ import annotations
 
@@ -48,8 +49,10 @@ def log(msg):
 
 def traffic_from_profile(path=TRAFFIC_FILE):
     """HBM bytes per gate+up launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
-    summary, each counter scaled by what it reads for a device copy of known size.
-    None when the summary is absent (counters cannot be read from inside this process)."""
+    summary: the launch's FETCH_SIZE scaled by what that counter reads for the read-only
+    calibration pass of known size (calibration_passes), its WRITE_SIZE by what that counter
+    reads for the write-only pass. None when the summary is absent (counters cannot be read
+    from inside this process)."""
     if not os.path.exists(path):
         return None
     vals = {}
@@ -58,9 +61,9 @@ def traffic_from_profile(path=TRAFFIC_FILE):
         if len(parts) == 2 and not line.startswith("#"):
             vals[parts[0]] = float(parts[1])
     try:
-        fetch = vals["fetch_kib"] * vals["copy_kib"] / vals["copy_fetch_kib"]
-        write = vals["write_kib"] * vals["copy_kib"] / vals["copy_write_kib"]
-    except KeyError:
+        fetch = vals["fetch_kib"] * vals["cal_kib"] / vals["cal_read_fetch_kib"]
+        write = vals["write_kib"] * vals["cal_kib"] / vals["cal_fill_write_kib"]
+    except (KeyError, ZeroDivisionError):
         return None
     return int(round((fetch + write) * 1024))
 
@@ -145,7 +148,8 @@ def run_block(te, torch, dev, layers, groups, B, K, V, steps, warmup, min_bytes=
 
     us_group, us_layer = {}, {}
     if per_launch:
-        reps = max(2, steps // copies)
+        # at least ~200 launches per figure, whatever the step count
+        reps = max(math.ceil(200 / copies), steps // copies)
 
         def per_launch_us(fn_for_copy):
             # one graph holding the launch for every copy (distinct weights back to back),
@@ -170,9 +174,29 @@ def run_block(te, torch, dev, layers, groups, B, K, V, steps, warmup, min_bytes=
     return sec, us_group, us_layer, copies
 
 
-def cpu_baseline(budget_s: float = 20.0):
-    """torch-CPU decode+restore+matmul (oracle/torch_cpu.py) of the 8B q_proj, K=3 MCG,
-    on all host cores; median over repeated runs within ~budget_s."""
+# CPU-baseline layers: (config, layer, n_out, k_in, K, codebook). Configurations 1 to 3 of
+# the benchmark per layer (the 8B block's v, o and up have the shapes of k, q and gate) and
+# one point of the bit-rate sweep.
+CPU_LAYERS = [
+    ("configs[0] SmolLM2-135M", "up_proj", 1536, 576, 3, "3inst"),
+    ("configs[1] Qwen3-1.7B MLP", "gate/up", 6144, 2048, 3, "mcg"),
+    ("configs[1] Qwen3-1.7B MLP", "down", 2048, 6144, 3, "mcg"),
+    ("configs[2] Qwen3-8B block", "q/o", 4096, 4096, 3, "mcg"),
+    ("configs[2] Qwen3-8B block", "k/v", 1024, 4096, 3, "mcg"),
+    ("configs[2] Qwen3-8B block", "gate/up", 12288, 4096, 3, "mcg"),
+    ("configs[2] Qwen3-8B block", "down", 4096, 12288, 3, "mcg"),
+    ("configs[4] sweep K=4", "gate/up", 12288, 4096, 4, "mcg"),
+]
+# how many times each 8B shape occurs in the block (q, k, v, o, gate, up, down)
+BLOCK_MULT = {"q/o": 2, "k/v": 2, "gate/up": 2, "down": 1}
+
+
+def cpu_baseline(budget_s: float = 30.0):
+    """The reference's decode-then-matmul restated in torch CPU ops (oracle/torch_cpu.py:
+    decode + restore + matmul, qtip.py:82-110, 262-268) on every host core, per
+    configuration and layer: (a) the whole call and (b) the matmul alone against a cached
+    W_hat, medians of repeated runs after a warm-up. The headline value is the 8B block's
+    packed bytes over the sum of its seven layers' (a) times."""
     import numpy as np
     import torch
     from oracle import torch_cpu as tc
@@ -182,27 +206,37 @@ def cpu_baseline(budget_s: float = 20.0):
     torch.set_num_threads(cores)
     log(f"[bench] cpu baseline on {cores} threads")
     log(torch.__config__.parallel_info())
-    n, k = 4096, 4096
-    bits, rec = tn.synthetic_record(n, k, 3, seed=7)
-    lut = tc.codebook_lut_torch("mcg")
-    x = torch.from_numpy(np.random.default_rng(0).standard_normal(k).astype(np.float16)).float()
-    tc.decode_matmul(bits, rec, x, lut)       # warm-up
-    times = []
     t_start = time.perf_counter()
-    while len(times) < 5 or (time.perf_counter() - t_start < budget_s and len(times) < 50):
-        t0 = time.perf_counter()
-        tc.decode_matmul(bits, rec, x, lut)
-        times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_start > budget_s and len(times) >= 3:
-            break
-    W = tc.w_hat(bits, rec, lut)
-    mm = []
-    for _ in range(5):
-        t0 = time.perf_counter()
-        _ = W @ x
-        mm.append(time.perf_counter() - t0)
-    med = statistics.median(times)
-    packed = n * k * 3 // 8
+    per_layer = []
+    block_s = 0.0
+    runs = 3
+    for cfg, layer, n, k, K, cb in CPU_LAYERS:
+        bits, rec = tn.synthetic_record(n, k, K, seed=n + k + K, codebook=cb)
+        lut = tc.codebook_lut_torch(cb)
+        x = torch.from_numpy(np.random.default_rng(0).standard_normal(k).astype(np.float16)).float()
+        tc.decode_matmul(bits, rec, x, lut)          # warm-up
+        full = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            tc.decode_matmul(bits, rec, x, lut)
+            full.append(time.perf_counter() - t0)
+        W = tc.w_hat(bits, rec, lut)
+        mm = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            _ = W @ x
+            mm.append(time.perf_counter() - t0)
+        a, b = statistics.median(full), statistics.median(mm)
+        pb = n * k * K // 8
+        per_layer.append({"config": cfg, "layer": layer, "shape": f"{n}x{k}", "K": K,
+                          "codebook": cb, "decode_restore_matmul_ms": round(a * 1e3, 2),
+                          "matmul_only_ms": round(b * 1e3, 3),
+                          "packed_GBps": round(pb / a / 1e9, 4)})
+        log(f"[bench] cpu {cfg} {layer} {n}x{k} K={K}: {a * 1e3:.1f} ms (matmul {b * 1e3:.2f} ms)")
+        if cfg.startswith("configs[2]"):
+            block_s += BLOCK_MULT[layer] * a
+    total_s = time.perf_counter() - t_start
+    block_bytes = sum(n * k * 3 // 8 for _, n, k in LAYERS)
     # the encoder row: the C restatement of the tail-biting Viterbi (oracle/viterbi.c,
     # OpenMP over tiles) on 4 tiles per core, K=3 MCG
     from oracle import viterbi as ov
@@ -212,12 +246,14 @@ def cpu_baseline(budget_s: float = 20.0):
     t0 = time.perf_counter()
     ov.viterbi_tb(wt, 3, lut_np)
     enc_s = time.perf_counter() - t0
-    return {"value": round(packed / med / 1e9, 4), "unit": "GB/s", "cores": cores,
+    return {"value": round(block_bytes / block_s / 1e9, 4), "unit": "GB/s", "cores": cores,
             "kind": "port",
-            "sample": f"Qwen3-8B q_proj 4096x4096 K=3 MCG, torch-CPU decode+restore+matmul "
-                      f"(oracle/torch_cpu.py), median of {len(times)} runs = {med * 1e3:.1f} ms; "
-                      f"matmul alone on cached W_hat {statistics.median(mm) * 1e3:.2f} ms",
-            "ms_per_layer": round(med * 1e3, 2),
+            "sample": f"torch-CPU decode+restore+matmul (oracle/torch_cpu.py) at batch 1, median "
+                      f"of {runs} runs per layer after a warm-up, {len(CPU_LAYERS)} layers in "
+                      f"{total_s:.1f} s; value = Qwen3-8B block packed bytes / sum of its seven "
+                      f"layers' times ({block_s * 1e3:.0f} ms)",
+            "us_per_block": round(block_s * 1e6, 1),
+            "per_layer": per_layer,
             "encode_tiles_per_s": round(wt.shape[0] / enc_s, 1),
             "encode_sample": f"oracle/viterbi.c tail-biting encode, K=3 MCG, {wt.shape[0]} tiles "
                              f"on {cores} threads: {enc_s:.2f} s"}
@@ -321,6 +357,48 @@ def batched_figure(te, torch, dev, bs, K, V, args):
     return out
 
 
+def sweep_point(te, torch, dev, K, V, B, args):
+    """One point of the bit-rate sweep: gate, up and down of the 8B block, one launch each,
+    at K bits, V weights per step and batch B (1, or a 512-token prefill), over >= 1 GB of
+    distinct weight copies. Roofline of the whole point: HBM on the packed bytes at batch 1,
+    fp16 MFMA on the algorithmic flops at 512."""
+    log(f"[bench] sweep K={K} V={V} batch={B}")
+    steps = max(20, args.steps) if B == 1 else 10
+    sec, sg, _, copies = run_block(te, torch, dev, MLP, [(n, (n,)) for n, _, _ in MLP], B, K, V,
+                                   steps, 3, per_launch=True)
+    pb = sum(n * k * K // 8 for _, n, k in MLP)
+    fl = block_flops(MLP, B)
+    gbs, tfl = pb / sec / 1e9, fl / sec / 1e12
+    if B == 1:
+        roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    else:
+        roof = {"bound": "mfma", "achieved": round(tfl, 2), "peak": MFMA_FP16_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(tfl / MFMA_FP16_PEAK_TFLOPS, 4)}
+    return {"K": K, "V": V, "batch": B, "steps": steps, "weight_copies": copies,
+            "us_gate_up_down": round(sec * 1e6, 2), "us_per_layer": sg,
+            "packed_GBps": round(gbs, 1), "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+            "tflops": round(tfl, 2), "roofline": roof}
+
+
+CAL_BYTES = 1 << 30
+
+
+def calibration_passes(torch, dev):
+    """Passes of known size for scaling the rocprofv3 HBM counters (run under --pmc, they
+    appear as their own dispatches): a read-only sum over 1 GiB (FETCH_SIZE of exactly 1 GiB
+    of reads, 4x the 256 MB MALL) and a fill of 1 GiB (WRITE_SIZE of 1 GiB of writes)."""
+    a = torch.ones(CAL_BYTES // 4, dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        s = a.sum()
+    for _ in range(3):
+        a.fill_(2.0)
+    torch.cuda.synchronize()
+    del a, s
+    torch.cuda.empty_cache()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -336,11 +414,11 @@ def main():
     ap.add_argument("--mma-f16", action="store_true",
                     help="the fp16-weight MFMA mode (TRELLIS_MMA_F16) for the block run (calls "
                          "on the batched path)")
-    ap.add_argument("--sweep", action="store_true", help="add the K x V sweep on the gate/up/down shapes")
+    ap.add_argument("--no-sweep", action="store_true",
+                    help="skip the K x V bit-rate sweep on the gate/up/down shapes")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the LM-head GEMV and embedding-row lookup figures")
-    ap.add_argument("--cpu-budget", type=float, default=20.0)
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -372,25 +450,9 @@ def main():
     batch64 = batched.get(64)
 
     sweep = None
-    if args.sweep:
-        sweep = []
-        for Ks in (2, 3, 4):
-            for Vs in (1, 2):
-                for Bs in (1, 512):
-                    log(f"[bench] sweep K={Ks} V={Vs} batch={Bs}")
-                    steps = args.steps if Bs == 1 else max(10, args.steps // 20)
-                    ssec, sg, _, _ = run_block(te, torch, dev, MLP,
-                                               [(n, (n,)) for n, _, _ in MLP], Bs, Ks, Vs,
-                                               steps, max(2, args.warmup // 5),
-                                               per_launch=True)
-                    pb = sum(n * k * Ks // 8 for _, n, k in MLP)
-                    fl = block_flops(MLP, Bs)
-                    sweep.append({"K": Ks, "V": Vs, "batch": Bs,
-                                  "us_gate_up_down": round(ssec * 1e6, 2),
-                                  "us_per_layer": sg,
-                                  "packed_GBps": round(pb / ssec / 1e9, 1),
-                                  "pct_of_hbm_peak": round(100 * pb / ssec / 1e9 / HBM_PEAK_GBS, 2),
-                                  "tflops": round(fl / ssec / 1e12, 2)})
+    if not args.no_sweep and B == 1:
+        sweep = [sweep_point(te, torch, dev, Ks, Vs, Bs, args)
+                 for Ks in (2, 3, 4) for Vs in (1, 2) for Bs in (1, 512)]
 
     extra = None
     if not args.no_extras and B == 1:
@@ -406,12 +468,7 @@ def main():
         extra["us_per_block_small_batch"] = small
         log(f"[bench] extras {extra}")
 
-    # known-size copy for the HBM-counter scale factor (FETCH_SIZE / WRITE_SIZE)
-    src = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
-    dst = torch.empty_like(src)
-    for _ in range(3):
-        dst.copy_(src)
-    torch.cuda.synchronize()
+    calibration_passes(torch, dev)
 
     out = {
         "metric": "3-bit decode-GEMV HBM GB/s (% of peak) + us/layer, Qwen3-8B shapes, batch 1/64",
@@ -445,7 +502,9 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_from_profile() if B == 1 and K == 3 and V == 1 else None,
                      "traffic_source": "profiles/gemv_gate_up_b1_traffic.txt (rocprofv3 "
-                                       "FETCH_SIZE/WRITE_SIZE, copy-scaled)",
+                                       "FETCH_SIZE / WRITE_SIZE of this launch, each scaled by "
+                                       "what it reads for a read-only / write-only pass of "
+                                       "known size)",
                      "kernel": f"gemv_kernel<K={K},MCG,V={V}> on the gate+up group "
                                "(2 x 12288x4096, one launch)" if B == 1 else
                                f"bgemm_kernel<K={K},MCG,V={V}> on the gate+up group",
@@ -454,7 +513,7 @@ def main():
     }
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline")
-        out["cpu_baseline"] = cpu_baseline(args.cpu_budget)
+        out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)
 
 

@@ -83,3 +83,44 @@ def test_validate_rejects_bad_v(te):
     rec = te.PackedRecord(32, 64, 3, bits, r.su, r.sv, r.isc, r.osc, float(r.scale), V=3)
     with pytest.raises(ValueError):
         rec.validate()
+
+
+def test_manifest_block_other_than_fit_is_rejected(te, tmp_path):
+    """The exporters write block = fit(k_in, 128) (export_packed.py:62) and this reader
+    restores with that block; a manifest naming another in-dim block is refused rather
+    than loaded into a linear that would restore its weights wrongly."""
+    import pytest
+    r = _rec(te, 32, 96, 3, 7)          # fit(96, 128) = 32
+    te.write_packed(str(tmp_path), {"l": r})
+    man = json.load(open(tmp_path / "manifest.json"))
+    assert man["l"]["block"] == 32
+    te.read_packed(str(tmp_path))        # the exporter's own value loads
+    man["l"]["block"] = 16
+    json.dump(man, open(tmp_path / "manifest.json", "w"))
+    with pytest.raises(ValueError, match="block"):
+        te.read_packed(str(tmp_path))
+    del man["l"]["block"]                # absent: the exporter's value is implied
+    json.dump(man, open(tmp_path / "manifest.json", "w"))
+    got, _, _ = te.read_packed(str(tmp_path))
+    assert np.array_equal(got["l"].bits, r.bits)
+
+
+def test_append_merges_shards_into_one_manifest(te, tmp_path):
+    """Shards written one call at a time join one manifest (export_packed_8b.py:271-276
+    merges its per-shard fragments); every entry keeps its own shard's offsets; a shard
+    name already in the manifest is refused."""
+    import pytest
+    a, b = _rec(te, 32, 48, 3, 21), _rec(te, 64, 32, 2, 22)
+    te.write_packed(str(tmp_path), {"l0.q.weight": a}, shard="layer_00.bin")
+    te.write_packed(str(tmp_path), {"l1.q.weight": b}, dense={"norm": np.ones(8, np.float16)},
+                    shard="layer_01.bin", append=True)
+    man = json.load(open(tmp_path / "manifest.json"))
+    assert man["l0.q.weight.bits"]["shard"] == "layer_00.bin"
+    assert man["l1.q.weight.bits"]["shard"] == "layer_01.bin"
+    assert man["l1.q.weight.bits"]["offset"] == 0
+    got, dense, _ = te.read_packed(str(tmp_path))
+    assert np.array_equal(got["l0.q.weight"].bits, a.bits)
+    assert np.array_equal(got["l1.q.weight"].bits, b.bits)
+    assert got["l1.q.weight"].K == 2 and dense["norm"].shape == (8,)
+    with pytest.raises(ValueError):
+        te.write_packed(str(tmp_path), {"x": a}, shard="layer_01.bin", append=True)

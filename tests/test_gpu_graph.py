@@ -68,3 +68,49 @@ def test_graph_replays_match_eager(te, gpu_device, batch, mma_f16):
         torch.cuda.synchronize()
         for a, b in zip(got, want):
             assert torch.equal(a, b), f"replay {rep}"
+
+
+def test_graph_survives_workspace_growth(te, gpu_device):
+    """A graph captured at batch 1, then an eager call at a larger batch that needs a larger
+    workspace: the linear swaps in a bigger workspace but keeps the one the graph holds
+    alive, so every later replay still writes its split-K partials and counters into
+    memory no other tensor owns, and still equals the eager batch-1 call."""
+    _say("[graph] workspace growth after capture")
+    bits, rec = tn.synthetic_record(1024, 2048, 3, seed=77)
+    lin = make_linear(te, bits, rec, gpu_device)
+    rng = np.random.default_rng(7)
+    x = torch.from_numpy(rng.standard_normal((1, 2048)).astype(np.float16)).to(gpu_device)
+    y = torch.empty((1, 1024), device=gpu_device)
+    lin.forward(x, out=y)
+    torch.cuda.synchronize()
+    ws_captured = lin._ws
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream(device=gpu_device)
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        lin.forward(x, out=y)
+    torch.cuda.current_stream().wait_stream(side)
+    with torch.cuda.graph(g):
+        lin.forward(x, out=y)
+    torch.cuda.synchronize()
+    xb = torch.from_numpy(rng.standard_normal((300, 2048)).astype(np.float16)).to(gpu_device)
+    yb = lin(xb)                                   # grows the workspace
+    assert lin._ws is not ws_captured and lin._ws.numel() > ws_captured.numel()
+    assert any(w is ws_captured for w in lin._ws_retired)
+    # churn the caching allocator: freed blocks would be handed out here
+    junk = [torch.full((ws_captured.numel(),), 255, dtype=torch.uint8, device=gpu_device)
+            for _ in range(4)]
+    for rep in range(3):
+        xin = torch.from_numpy(rng.standard_normal((1, 2048)).astype(np.float16)).to(gpu_device)
+        x.copy_(xin)
+        g.replay()
+        torch.cuda.synchronize()
+        got = y.clone()
+        want = lin(xin)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"replay {rep}"
+        assert tn.rel_err(got.cpu().numpy(), tn.packed_linear_ref(bits, rec, xin.cpu().numpy())) < 1e-3
+    for j in junk:
+        assert torch.all(j == 255)
+    want_b = tn.packed_linear_ref(bits, rec, xb.cpu().numpy())
+    assert tn.rel_err(yb.cpu().numpy(), want_b) < 1e-3

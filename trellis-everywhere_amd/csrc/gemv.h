@@ -31,6 +31,32 @@
 
 namespace trellis {
 
+// Split-K publication: why relaxed agent-scope atomics plus a vmcnt wait order the partial
+// sums on gfx950 (both epilogues below use this pattern).
+//
+// The C++/HIP memory model alone does not promise it: the ticket's fetch_add is relaxed, so
+// formally nothing orders a workgroup's partial-sum stores before it. The ordering comes
+// from how gfx950 executes these operations:
+//   1. A relaxed agent-scope atomic store is a global store with the coherence bits set
+//      (sc1): it does not stay in the XCD's own, non-coherent L2 but is written through to
+//      the device-coherent point (memory side of the Infinity Fabric / MALL), where every
+//      XCD reads the same bytes.
+//   2. `s_waitcnt vmcnt(0)` holds the wave until each of its stores is acknowledged by that
+//      point, i.e. performed for every agent. Only then is the ticket's atomic issued.
+//   3. The fetch_add is itself performed at the coherent point, so the arrivals form one
+//      order there; the workgroup that reads S - 1 arrives after every other slice's
+//      partial sums were performed.
+//   4. The last workgroup reads the partials with relaxed agent-scope atomic loads (sc1:
+//      they bypass the L2's possibly stale lines) issued only after its fetch_add has
+//      returned (the branch on the returned value depends on it), so they read what was
+//      performed before that fetch_add.
+// A formal release/acquire pair (acq_rel on the fetch_add) compiles to a write-back of the
+// XCD's whole L2 before the atomic and an invalidate after it (buffer_wbl2 sc1 /
+// buffer_inv sc1); a device-scope fence here (__threadfence, the same write-back and
+// invalidate) measured about ten times slower than this epilogue. The pattern above moves
+// only the partial sums through the coherent point. Every step is exercised by the
+// determinism tests (repeated calls bit-identical at batch 1, 16 and 64).
+
 constexpr int GEMV_WAVES = 16;    // two waves per 16-row band: 128 rows per workgroup
 constexpr int GEMV_MAX_KR = 256;  // tile columns per k-range (4096 activations)
 // tile columns per k-range with NB batch rows: the rows' folded activations of one k-range
@@ -315,7 +341,8 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
       t1 = tt[0][n][lane + 64] + tt[1][n][lane + 64];
     }
     if (m.S > 1) {
-      // partial sums [block][slice][NB][128]
+      // partial sums [block][slice][NB][128]; published as the comment at the top of this
+      // file explains (write-through atomic stores, acknowledged before the ticket)
       float* mypart = m.part + (static_cast<size_t>(ob) * m.S + sl) * NB * 128 + n * 128;
       if (mine) {
         __hip_atomic_store(mypart + lane, t0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -388,7 +415,8 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
     t1[n] = tt[0][n][lane + 64] + tt[1][n][lane + 64];
   }
   if (m.S > 1) {
-    // partial sums [block][slice][NB][128]
+    // partial sums [block][slice][NB][128], published as the comment at the top of this
+    // file explains (write-through atomic stores, acknowledged before the ticket)
     float* mypart = m.part + (static_cast<size_t>(ob) * m.S + sl) * NB * 128;
 #pragma unroll
     for (int n = 0; n < NB; ++n) {

@@ -107,12 +107,23 @@ class _Blob:
 
 
 def write_packed(out_dir: str, records: dict, dense: dict | None = None,
-                 config: dict | None = None, shard: str | None = None) -> None:
+                 config: dict | None = None, shard: str | None = None,
+                 append: bool = False) -> None:
     """Write records ({name: PackedRecord}) and optional dense f16 tensors in the
     reference layout. With `shard`, the blob is written as that file and every entry
-    carries "shard" (export_packed_8b.py:65-81); otherwise weights.bin."""
+    carries "shard" (export_packed_8b.py:65-81); otherwise weights.bin. With `append`,
+    the entries join those of an existing manifest.json in out_dir (one shard per call,
+    merged into one manifest as export_packed_8b.py:271-276 merges its shard fragments)."""
     os.makedirs(out_dir, exist_ok=True)
     blob = _Blob()
+    mpath = os.path.join(out_dir, "manifest.json")
+    if append and os.path.exists(mpath):
+        with open(mpath) as f:
+            old = json.load(f)
+        target = shard or "weights.bin"
+        if any(m.get("shard", "weights.bin") == target for m in old.values()):
+            raise ValueError(f"{target} already holds entries of this manifest")
+        blob.man.update(old)
     for name, r in records.items():
         r.validate()
         blob.put(f"{name}.bits", r.bits, np.uint32, shard)
@@ -134,7 +145,7 @@ def write_packed(out_dir: str, records: dict, dense: dict | None = None,
         blob.put(name, t, np.float16, shard)
     with open(os.path.join(out_dir, shard or "weights.bin"), "wb") as f:
         f.write(bytes(blob.buf))
-    with open(os.path.join(out_dir, "manifest.json"), "w") as f:
+    with open(mpath, "w") as f:
         json.dump(blob.man, f)
     if config is not None:
         with open(os.path.join(out_dir, "config.json"), "w") as f:
@@ -169,6 +180,14 @@ def read_packed(model_dir: str):
             blob = memoryview(f.read())
         for name, m in entries.items():
             if m.get("quant"):
+                # the in-dim Hadamard block this build applies is fit(k_in, 128), the
+                # block every exporter writes (export_packed.py:62); the reference's loader
+                # takes the manifest's value (web/packed.js:57, 166), so a manifest naming
+                # another block describes weights this reader would restore wrongly
+                want = fit_block(int(m["k_in"]), 128)
+                if int(m.get("block", want)) != want:
+                    raise ValueError(f"{name}: manifest block {m['block']} != fit(k_in={m['k_in']}, "
+                                     f"128) = {want}; only the exporters' block is supported")
                 sub = {k: man[f"{name}.{k}"] for k in SUBKEYS}
                 bits = np.array(_raw(blob, sub["bits"]), np.uint32)
                 rec = PackedRecord(

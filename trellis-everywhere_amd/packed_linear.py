@@ -20,6 +20,20 @@ def _ptr(t: torch.Tensor) -> int:
     return t.data_ptr()
 
 
+def _grow_workspace(owner, need: int) -> torch.Tensor:
+    """The owner's workspace, replaced by a larger zero-filled one when `need` exceeds it
+    (every call leaves its counters at zero again, so a workspace is zero-filled once).
+    A replaced buffer is kept alive with its owner, never freed: a HIP graph captured
+    earlier still holds its address, and its replays write split-K partials and counters
+    there; released to the caching allocator, that memory could belong to another tensor
+    by the next replay."""
+    if owner._ws is None or owner._ws.numel() < need:
+        if owner._ws is not None:
+            owner._ws_retired.append(owner._ws)
+        owner._ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=owner.device)
+    return owner._ws
+
+
 class PackedLinear:
     """One packed trellis linear resident on a GPU.
 
@@ -74,6 +88,7 @@ class PackedLinear:
             self.n_out, self.k_in, self.K, self.V, _capi.CB_IDS[self.codebook],
             self.block_in, self.block_out, self.nwords)
         self._ws = None
+        self._ws_retired = []
 
     @property
     def packed_bytes(self) -> int:
@@ -86,12 +101,14 @@ class PackedLinear:
         _capi.check(lib.trellis_workspace_bytes(ctypes.byref(self.desc), int(batch), ctypes.byref(n)))
         return int(n.value)
 
+    def reserve(self, max_batch: int) -> torch.Tensor:
+        """Size the workspace once for calls of up to `max_batch` rows. Call it before
+        capturing calls in a HIP graph: a captured launch keeps the workspace's address,
+        so a graph stays valid only while that buffer lives (see _workspace)."""
+        return _grow_workspace(self, self.workspace_bytes(max_batch))
+
     def _workspace(self, batch: int) -> torch.Tensor:
-        need = self.workspace_bytes(batch)
-        if self._ws is None or self._ws.numel() < need:
-            # zero-filled once; every call leaves the tickets at zero again
-            self._ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=self.device)
-        return self._ws
+        return _grow_workspace(self, self.workspace_bytes(batch))
 
     # ------------------------------------------------------------------ calls
     def forward(self, x: torch.Tensor, out: torch.Tensor | None = None,
@@ -120,6 +137,9 @@ class PackedLinear:
         y2 = out.view(B, self.n_out) if out.dim() == 1 else out
         if y2.dtype not in (torch.float16, torch.float32) or y2.stride(1) != 1:
             raise ValueError("out must be fp16/fp32 with unit column stride")
+        if B == 0:
+            # no rows, nothing to launch (the C ABI rejects a batch of 0)
+            return out
         ws = workspace if workspace is not None else self._workspace(B)
         stream = torch.cuda.current_stream(self.device).cuda_stream
         st = lib.trellis_packed_linear_ex(
@@ -188,6 +208,7 @@ class PackedGroup:
         self._dptrs = (ctypes.POINTER(_capi.TrellisDesc) * n)(
             *[ctypes.pointer(self._descs[i]) for i in range(n)])
         self._ws = None
+        self._ws_retired = []
 
     def workspace_bytes(self, batch: int) -> int:
         lib = _capi.load()
@@ -196,11 +217,12 @@ class PackedGroup:
                                                       ctypes.byref(nbytes)))
         return int(nbytes.value)
 
+    def reserve(self, max_batch: int) -> torch.Tensor:
+        """As PackedLinear.reserve: size the group's workspace once, before capture."""
+        return _grow_workspace(self, self.workspace_bytes(max_batch))
+
     def _workspace(self, batch: int) -> torch.Tensor:
-        need = self.workspace_bytes(batch)
-        if self._ws is None or self._ws.numel() < need:
-            self._ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=self.device)
-        return self._ws
+        return _grow_workspace(self, self.workspace_bytes(batch))
 
     def forward(self, xs, outs=None, out_dtype: torch.dtype = torch.float32,
                 mma_f16: bool = False):
@@ -228,6 +250,9 @@ class PackedGroup:
         if any(y.dtype != ydt or y.stride(1) != 1 for y in y2) or ydt not in (torch.float16,
                                                                                torch.float32):
             raise ValueError("outputs must share an fp16/fp32 dtype with unit column stride")
+        if B == 0:
+            # no rows: every member's output is [0, n_i], nothing to launch
+            return outs
         ws = self._workspace(B)
         xp = (ctypes.c_void_p * n)(*[x.data_ptr() for x in x2])
         yp = (ctypes.c_void_p * n)(*[y.data_ptr() for y in y2])
