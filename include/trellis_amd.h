@@ -55,7 +55,8 @@ typedef enum trellis_status {
   TRELLIS_ERR_RANGE = 12,      /* tile range outside the matrix */
   TRELLIS_ERR_LAUNCH = 13,     /* the HIP runtime rejected a launch */
   TRELLIS_ERR_GROUP = 14,      /* group of 0 or more than 8 linears, or mixed K / V / codebook */
-  TRELLIS_ERR_FLAGS = 15       /* unknown bits in the flags of an _ex call */
+  TRELLIS_ERR_FLAGS = 15,      /* unknown bits in the flags of an _ex call */
+  TRELLIS_ERR_SCRATCH = 16     /* a _noalloc call needs more than TRELLIS_NOALLOC_SCRATCH_BYTES */
 } trellis_status;
 
 /* Flags of trellis_packed_linear_ex / trellis_packed_linear_group_ex. */
@@ -139,6 +140,23 @@ int trellis_packed_linear_group_ex(const trellis_desc *const *W, int count,
                                    const void *const *x, const int64_t *ldx, int batch,
                                    int x_dtype, void *const *y, const int64_t *ldy, int y_dtype,
                                    void *workspace, size_t ws_bytes, int flags, void *stream);
+
+/* No counterpart in the reference: for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * semantics, validation and kernels as trellis_packed_linear_group_ex, but no workspace
+ * argument: the workspace is a static device array of TRELLIS_NOALLOC_SCRATCH_BYTES that
+ * the library holds on every GPU it runs on until the process ends. The call allocates
+ * nothing (no hipMalloc, no allocating library routine). A call whose plan needs more
+ * workspace than that returns TRELLIS_ERR_SCRATCH (the Qwen3-8B block linears fit up to a
+ * batch of 128 rows). Every call on a GPU shares that GPU's array: the split-K counters a
+ * call needs are zeroed by a small kernel at its start, and calls that overlap on one GPU
+ * (on different streams, or from several threads) race and must be serialized by the
+ * caller. */
+#define TRELLIS_NOALLOC_SCRATCH_BYTES (32u << 20)
+int trellis_packed_linear_group_noalloc(const trellis_desc *const *W, int count,
+                                        const void *const *x, const int64_t *ldx, int batch,
+                                        int x_dtype, void *const *y, const int64_t *ldy,
+                                        int y_dtype, int flags, void *stream);
 
 /* Decode z-space tiles [tile_begin, tile_begin+ntiles) to fp32, 256 values per tile in
  * tile order t = (row%16)*16 + col%16. The bit-exact probe of the decode: restates

@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol(te):
 
 def test_strerror_names_every_status(te):
     lib = te.library()
-    for code in range(0, 16):
+    for code in range(0, 17):
         assert lib.trellis_strerror(code).decode() not in ("", "unknown trellis status")
     assert lib.trellis_strerror(99).decode() == "unknown trellis status"
 
@@ -145,3 +145,28 @@ def test_packed_linear_lives_on_a_gpu(te):
                         float(rec.scale), codebook=rec.codebook, V=rec.V)
     with pytest.raises(ValueError):
         te.PackedLinear(r, device="cpu")
+
+
+def test_noalloc_rejects_before_launch(te):
+    """trellis_packed_linear_group_noalloc validates like the _ex entry point, and refuses
+    a plan larger than its static scratch (TRELLIS_ERR_SCRATCH) before touching the GPU."""
+    lib = te.library()
+    d = _desc(te)
+    arr = (ctypes.POINTER(te._capi.TrellisDesc) * 1)(ctypes.pointer(d))
+    xp = (ctypes.c_void_p * 1)(16)
+    ld = (ctypes.c_int64 * 1)(256)
+    ldy = (ctypes.c_int64 * 1)(128)
+    f = lib.trellis_packed_linear_group_noalloc
+    assert f(arr, 1, xp, ld, 2, 0, xp, ldy, 0, 2, None) == 15          # unknown flag
+    assert f(arr, 1, xp, ld, 0, 0, xp, ldy, 0, 0, None) == 11          # batch 0
+    assert f(arr, 1, xp, ld, 2, 7, xp, ldy, 0, 0, None) == 9           # dtype
+    assert f(arr, 0, xp, ld, 2, 0, xp, ldy, 0, 0, None) == 1           # empty group
+    big = _desc(te, n_out=12288, k_in=4096)
+    barr = (ctypes.POINTER(te._capi.TrellisDesc) * 1)(ctypes.pointer(big))
+    bld = (ctypes.c_int64 * 1)(4096)
+    bldy = (ctypes.c_int64 * 1)(12288)
+    n = ctypes.c_size_t(0)
+    assert lib.trellis_workspace_bytes(ctypes.byref(big), 4096, ctypes.byref(n)) == 0
+    assert n.value > te._capi.NOALLOC_SCRATCH_BYTES
+    assert f(barr, 1, xp, bld, 4096, 1, xp, bldy, 0, 0, None) == 16
+    assert "scratch" in lib.trellis_strerror(16).decode()

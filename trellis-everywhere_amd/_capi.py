@@ -22,8 +22,11 @@ STATUS_NAMES = {
     4: "TRELLIS_ERR_K", 5: "TRELLIS_ERR_V", 6: "TRELLIS_ERR_CODEBOOK", 7: "TRELLIS_ERR_NWORDS",
     8: "TRELLIS_ERR_ALIGN", 9: "TRELLIS_ERR_DTYPE", 10: "TRELLIS_ERR_WORKSPACE",
     11: "TRELLIS_ERR_BATCH", 12: "TRELLIS_ERR_RANGE", 13: "TRELLIS_ERR_LAUNCH",
-    14: "TRELLIS_ERR_GROUP", 15: "TRELLIS_ERR_FLAGS",
+    14: "TRELLIS_ERR_GROUP", 15: "TRELLIS_ERR_FLAGS", 16: "TRELLIS_ERR_SCRATCH",
 }
+
+# TRELLIS_NOALLOC_SCRATCH_BYTES: the static workspace of trellis_packed_linear_group_noalloc
+NOALLOC_SCRATCH_BYTES = 32 << 20
 
 # enum trellis_flags
 MMA_F16 = 1
@@ -33,7 +36,8 @@ EXPORTED = ("trellis_workspace_bytes", "trellis_packed_linear", "trellis_decode_
             "trellis_strerror", "trellis_version", "trellis_workspace_bytes_group",
             "trellis_packed_linear_group", "trellis_embed_rows",
             "trellis_encode_workspace_bytes", "trellis_encode_tiles",
-            "trellis_packed_linear_ex", "trellis_packed_linear_group_ex")
+            "trellis_packed_linear_ex", "trellis_packed_linear_group_ex",
+            "trellis_packed_linear_group_noalloc")
 
 
 class TrellisLibraryMissing(RuntimeError):
@@ -106,6 +110,10 @@ def load(path: str | None = None):
                                                    ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t,
                                                    ctypes.c_int, ctypes.c_void_p]
     lib.trellis_packed_linear_group_ex.restype = ctypes.c_int
+    lib.trellis_packed_linear_group_noalloc.argtypes = [ctypes.POINTER(D), ctypes.c_int, PP, I64P,
+                                                        ctypes.c_int, ctypes.c_int, PP, I64P,
+                                                        ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    lib.trellis_packed_linear_group_noalloc.restype = ctypes.c_int
     lib.trellis_decode_tiles.argtypes = [D, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p,
                                          ctypes.c_void_p]
     lib.trellis_decode_tiles.restype = ctypes.c_int

@@ -8,6 +8,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 
 #include "trellis_amd.h"
 #include "decode.h"
@@ -41,6 +42,13 @@ __global__ __launch_bounds__(256) void decode_tiles_kernel(const uint32_t* __res
   for (int q = 0; q < 4; ++q) v[q] = cb_exact<CB>(raw[q]);
   *reinterpret_cast<float4*>(out + static_cast<size_t>(lt) * 256 + 16 * r + 4 * g) =
       make_float4(v[0], v[1], v[2], v[3]);
+}
+
+// Zero n words (the split-K ticket header of a call on the static scratch below). A kernel,
+// not hipMemsetAsync, so that a caller may capture the call in a HIP graph.
+__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* __restrict__ p, unsigned n) {
+  const unsigned i = blockIdx.x * 256u + threadIdx.x;
+  if (i < n) p[i] = 0u;
 }
 
 // ---------------------------------------------------------------- validation
@@ -91,6 +99,7 @@ struct GroupPlan {
   int folds;           // x-fold jobs over the group
   int n_ob[MAX_GROUP], S[MAX_GROUP];
   size_t off_tickets[MAX_GROUP], off_part[MAX_GROUP], off_xf[MAX_GROUP];
+  size_t header;       // bytes of the ticket header at the start of the workspace
   size_t ws;           // workspace bytes
 };
 
@@ -239,6 +248,7 @@ GroupPlan group_plan(const trellis_desc* const* W, int count, int batch, bool f1
     p.off_tickets[i] = p.ws;
     p.ws += align256(static_cast<size_t>(p.n_ob[i]) * 4);
   }
+  p.header = p.ws;
   // partial sums per (block, slice): the gemv's NB batch rows, or bgemm's 16 * NC
   const int part_cols = p.gemv ? gemv_nb(batch) : 16 * p.nc;
   for (int i = 0; i < count; ++i) {
@@ -384,6 +394,9 @@ const char* trellis_strerror(int status) {
     case TRELLIS_ERR_LAUNCH: return "HIP kernel launch failed";
     case TRELLIS_ERR_GROUP: return "a group holds 1..8 linears sharing K, V and codebook";
     case TRELLIS_ERR_FLAGS: return "unknown flag bits";
+    case TRELLIS_ERR_SCRATCH:
+      return "the call needs more workspace than the no-allocation entry point's static scratch "
+             "(TRELLIS_NOALLOC_SCRATCH_BYTES)";
     default: return "unknown trellis status";
   }
 }
@@ -492,10 +505,43 @@ int trellis_encode_tiles(const float* w, uint32_t ntiles, int K, int codebook, u
   }
 }
 
-int trellis_packed_linear_group_ex(const trellis_desc* const* W, int count, const void* const* x,
-                                   const int64_t* ldx, int batch, int x_dtype, void* const* y,
-                                   const int64_t* ldy, int y_dtype, void* workspace,
-                                   size_t ws_bytes, int flags, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// The static scratch of trellis_packed_linear_group_noalloc: a workspace that no call
+// allocates. Each GPU the library runs on holds its own copy until the process ends. Its
+// host-side name is not a device address: host code uses only the per-device address that
+// hipGetSymbolAddress returns (scratch_ptr).
+constexpr size_t NOALLOC_SCRATCH_BYTES = TRELLIS_NOALLOC_SCRATCH_BYTES;
+__device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[MAX_DEVICES] = {};
+
+// The current device's address of `scratch`, looked up once per device (that device
+// current) and kept.
+int scratch_ptr(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return TRELLIS_ERR_LAUNCH;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return TRELLIS_ERR_LAUNCH;
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return TRELLIS_OK;
+}
+
+// trellis_packed_linear_group_ex, and with noalloc its variant on the static scratch: the
+// plan must fit NOALLOC_SCRATCH_BYTES, and the ticket header, which an earlier call on the
+// scratch may have covered with its data, is cleared before the launches.
+int packed_linear_group(const trellis_desc* const* W, int count, const void* const* x,
+                        const int64_t* ldx, int batch, int x_dtype, void* const* y,
+                        const int64_t* ldy, int y_dtype, void* workspace, size_t ws_bytes,
+                        int flags, void* stream, bool noalloc) {
   int v = validate_group(W, count);
   if (v) return v;
   if (flags & ~TRELLIS_MMA_F16) return TRELLIS_ERR_FLAGS;
@@ -518,6 +564,12 @@ int trellis_packed_linear_group_ex(const trellis_desc* const* W, int count, cons
       return TRELLIS_ERR_SHAPE;
   }
   const GroupPlan p = group_plan(W, count, batch, f16);
+  if (noalloc) {
+    if (p.ws > NOALLOC_SCRATCH_BYTES) return TRELLIS_ERR_SCRATCH;
+    v = scratch_ptr(&workspace);
+    if (v) return v;
+    ws_bytes = NOALLOC_SCRATCH_BYTES;
+  }
   if (!workspace || ws_bytes < p.ws) return TRELLIS_ERR_WORKSPACE;
   if (reinterpret_cast<uintptr_t>(workspace) % 256) return TRELLIS_ERR_ALIGN;
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -574,6 +626,18 @@ int trellis_packed_linear_group_ex(const trellis_desc* const* W, int count, cons
                          "items=%d S0=%d ws=%zu\n",
                  batch, count, p.gemv ? "gemv" : f16 ? "bgemm-f16" : "bgemm", p.kr, p.kc, p.nc,
                  p.ncb, p.total, p.S[0], p.ws);
+  if (noalloc && p.gemv) {
+    // only the decode-GEMV's split-K tickets must start at zero (the batched path writes
+    // its folded activations and partial sums before reading them)
+    bool tickets = false;
+    for (int i = 0; i < count; ++i) tickets = tickets || p.S[i] > 1;
+    const unsigned words = static_cast<unsigned>(p.header / 4);
+    if (tickets && words > 0) {
+      hipLaunchKernelGGL(zero_words_kernel, dim3((words + 255) / 256), dim3(256), 0, st,
+                         static_cast<uint32_t*>(workspace), words);
+      if (hipGetLastError() != hipSuccess) return TRELLIS_ERR_LAUNCH;
+    }
+  }
   const size_t xes = g.x_f16 ? 2 : 4, yes = g.y_f16 ? 2 : 4;
   for (int b0 = 0; b0 < batch; b0 += p.nb) {
     g.batch = batch - b0 < p.nb ? batch - b0 : p.nb;
@@ -589,6 +653,26 @@ int trellis_packed_linear_group_ex(const trellis_desc* const* W, int count, cons
     if (v) return v;
   }
   return TRELLIS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int trellis_packed_linear_group_ex(const trellis_desc* const* W, int count, const void* const* x,
+                                   const int64_t* ldx, int batch, int x_dtype, void* const* y,
+                                   const int64_t* ldy, int y_dtype, void* workspace,
+                                   size_t ws_bytes, int flags, void* stream) {
+  return packed_linear_group(W, count, x, ldx, batch, x_dtype, y, ldy, y_dtype, workspace,
+                             ws_bytes, flags, stream, false);
+}
+
+int trellis_packed_linear_group_noalloc(const trellis_desc* const* W, int count,
+                                        const void* const* x, const int64_t* ldx, int batch,
+                                        int x_dtype, void* const* y, const int64_t* ldy,
+                                        int y_dtype, int flags, void* stream) {
+  return packed_linear_group(W, count, x, ldx, batch, x_dtype, y, ldy, y_dtype, nullptr, 0,
+                             flags, stream, true);
 }
 
 int trellis_packed_linear_group(const trellis_desc* const* W, int count, const void* const* x,
