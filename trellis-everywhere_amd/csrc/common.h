@@ -69,6 +69,32 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, unsigned bytes) {
 constexpr unsigned RSRC_OOB = 0x40000000u;   // an offset past every buffer made here
 constexpr int AUX_NT = 2;                    // nontemporal cache policy (gfx94x/gfx950)
 
+// LDS byte address of a shared-memory pointer.
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+  return static_cast<unsigned>(reinterpret_cast<size_t>(
+      (__attribute__((address_space(3))) void*)(const_cast<void*>(p))));
+}
+
+// One 16-byte global -> LDS load per lane (gfx950 buffer_load_dwordx4 ... lds, nontemporal):
+// the 16 bytes at byte offset `voff` of the buffer (zeros past its end) land at LDS byte
+// address `lds_base` + 16 * lane; lds_base is wave-uniform (it goes to M0, which is saved
+// and restored). Written as inline assembly because the compiler's wait-count pass cannot
+// tell which LDS bytes such a load writes, and puts a wait for every outstanding load in
+// front of each later LDS read; the caller waits for these loads itself (s_waitcnt vmcnt).
+// Loads complete in issue order, so the compiler's own waits for earlier loads stay
+// correct (they may wait longer than needed, never shorter).
+__device__ __forceinline__ void load_lds16(rsrc_t r, unsigned lds_base, unsigned voff) {
+  unsigned saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "buffer_load_dwordx4 %2, %3, 0 offen nt lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds_base), "v"(voff), "s"(r)
+      : "memory");
+}
+
 // Activation i of an f16 or f32 array, read as the aligned u32 word holding it so the
 // load is branch-free (f16 arrays must be 4-byte aligned with an even row stride).
 __device__ __forceinline__ uint32_t load_act_word(const void* p, long long i, int is_f16) {

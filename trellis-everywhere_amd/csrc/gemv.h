@@ -12,9 +12,11 @@
 //     k-range of `kr` tile columns, run by one 16-wave workgroup (one per CU): waves w and
 //     w + 8 own band w, each for half of the k-range, so every wave of a CU starts together
 //     and none runs alone at the end.
-//   * Each wave streams its half-band in stages of KC tiles. GEMV_PF stages are in flight
-//     in registers (coalesced 16-byte loads); the current stage is copied to a wave-private
-//     LDS buffer and decoded from there, so no barrier is needed in the main loop.
+//   * Each wave streams its half-band in stages of KC tiles through a wave-private ring of
+//     two stages in LDS: gfx950's 16-byte buffer loads write each lane's chunk straight
+//     into the ring (no VGPR staging, no LDS store instruction), one stage stays in flight
+//     while the other is decoded, and the wave waits only on its own loads, so no barrier
+//     is needed.
 //   * Tiles are decoded GEMV_G at a time into separate A registers before their MFMAs are
 //     issued: a decode then never waits for an MFMA to release its operands.
 //   * The activation fold xf = Hb_k(isc_scaled * su * x) of the k-range (every batch row)
@@ -62,23 +64,46 @@ constexpr int GEMV_MAX_KR = 256;  // tile columns per k-range (4096 activations)
 // tile columns per k-range with NB batch rows: the rows' folded activations of one k-range
 // live in LDS as (x, x) pairs, 64 bytes per tile column and row
 __host__ __device__ constexpr int gemv_kr_max(int nb) { return nb <= 4 ? GEMV_MAX_KR : nb <= 8 ? 128 : 96; }
-constexpr int GEMV_PF = 2;        // pipeline stages in flight per wave
 constexpr int GEMV_G = 4;         // tiles decoded before their MFMAs are issued
+constexpr int GEMV_LDS = 160 * 1024;   // LDS bytes per CU (one workgroup per CU)
 
-template <int K, int CB, int V, int KC, int PF, int NB>
+// words of one wave's ring slot (a stage of KC tiles: every lane's 16-byte chunks, 1 KB per
+// load instruction), and the rows' folded activations per batch row (8 mod 64 words apart)
+__host__ __device__ constexpr int gemv_swp(int K, int KC) { return ((KC * 8 * K / 4 + 63) / 64) * 256; }
+__host__ __device__ constexpr int gemv_xrow(int nb) { return nb > 1 ? gemv_kr_max(nb) * 16 + 8 : gemv_kr_max(nb) * 16; }
+// stages in each wave's LDS ring: two (one decoded while the next is in flight). Deeper
+// rings measured slower on the 8B block at batch 1 (four stages: 59.3 us against 57.8, the
+// register-staged loads this ring replaced: 58.4), as did 32-tile stages.
+constexpr int GEMV_NS = 2;
+__host__ __device__ constexpr int gemv_lds_bytes(int K, int KC, int nb) {
+  return 4 * (GEMV_WAVES * GEMV_NS * gemv_swp(K, KC) + nb * gemv_xrow(nb) + 2 * nb * 128 +
+              gemv_kr_max(nb) / 8 + 4);
+}
+
+// s_waitcnt for the vector-memory counter only (expcnt and lgkmcnt at their maxima)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int K, int CB, int V, int KC, int NB>
 __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
   constexpr int NWK = 8 * K;                 // words per tile
   constexpr int SW = KC * NWK;               // words per wave-stage
   constexpr int CH = SW / 4;                 // 16-byte chunks per wave-stage
   constexpr int LOADS = (CH + 63) / 64;      // chunks per lane
   constexpr int CPT = NWK / 4;               // chunks per tile
-  constexpr int SWP = LOADS * 256;           // words per wave buffer: every lane's chunks
+  constexpr int SWP = gemv_swp(K, KC);       // words per ring slot: every lane's chunks
+  constexpr int NS = GEMV_NS;                // ring slots per wave
   constexpr int KRM = gemv_kr_max(NB);       // tile columns per k-range (max)
   constexpr int FCH = (KRM * 16 / 128 + GEMV_WAVES - 1) / GEMV_WAVES;  // fold chunks per wave
   // folded activations of the NB batch rows, rows 8 mod 64 words apart (bank spread)
-  constexpr int XROW = NB > 1 ? KRM * 16 + 8 : KRM * 16;
+  constexpr int XROW = gemv_xrow(NB);
   static_assert(NB <= GEMV_WAVES, "one wave per batch row in the epilogue");
-  __shared__ __align__(16) uint32_t stg[GEMV_WAVES * SWP];
+  static_assert(SWP == LOADS * 256, "ring slot layout");
+  static_assert(gemv_lds_bytes(K, KC, NB) <= GEMV_LDS, "ring, activations and sums fit the LDS");
+  __shared__ __align__(16) uint32_t stg[GEMV_WAVES * NS * SWP];
   __shared__ __align__(16) uint32_t xs[NB * XROW];
   __shared__ float tt[2][NB][128];
   __shared__ unsigned ready[KRM / 8];   // per 128-column chunk of xs: rows folded
@@ -102,7 +127,8 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
   const int s_begin = half ? s_mid : 0, s_end = half ? nst : s_mid;
   const int rows = min(128, m.n - ob * 128);
   const int band = ob * 8 + min(bl, rows / 16 - 1);
-  uint32_t* mystg = stg + wave * SWP;
+  uint32_t* myring = stg + wave * NS * SWP;
+  const unsigned ring_base = __builtin_amdgcn_readfirstlane(lds_addr(myring));
   const int kcols = ntl * 16;
   const int nch = (kcols + 127) / 128;
   const int nbv = NB > 1 ? min(NB, g.batch) : 1;     // batch rows of the call (<= NB)
@@ -113,7 +139,7 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
   // flight is static and each wait covers only the loads it needs), and per-lane offsets
   // are fixed while the per-stage part is one add. Order: output scales of the block
   // (used at the end), the fold's inputs (chunks w and w + GEMV_WAVES of the k-range),
-  // then the first PF stages of packed words.
+  // then the first NS stages of packed words.
   const rsrc_t r_sv = make_rsrc(m.sv + ob * 128, rows * 4);
   const rsrc_t r_osc = make_rsrc(m.osc + ob * 128, rows * 4);
   const int xsh = g.x_f16 ? 1 : 2;                   // log2 bytes per activation
@@ -166,8 +192,10 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
   // keeps the fold's loads ahead of the packed words in issue order
   asm volatile("" ::: "memory");
   // byte offset of this lane's 16-byte chunk within a stage (chunks past the stage's last
-  // are pointed out of range), and of stage s within the band's k-range
-  u32x4_t R[PF][LOADS];
+  // are pointed out of range), and of stage s within the band's k-range. Load q of a stage
+  // writes the lanes' chunks lane + 64 q, 16 bytes each, to words 256 q + 4 lane of the
+  // stage's ring slot (the slot base is wave-uniform: it goes to M0), so the slot holds the
+  // stage's tiles one after another, NWK words each.
   unsigned lo_q[LOADS];
 #pragma unroll
   for (int q = 0; q < LOADS; ++q) {
@@ -175,18 +203,17 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
     lo_q[q] = CH % 64 == 0 || ch < CH ? static_cast<unsigned>(((ch / CPT) * NWK + 4 * (ch % CPT)) * 4)
                                       : RSRC_OOB;
   }
-  auto load_stage = [&](int s, u32x4_t (&dst)[LOADS]) {
+  auto load_stage = [&](int s) {
     // a stage past the wave's last one (prefetch beyond the end) reads nothing
     const unsigned soff = s < s_end ? static_cast<unsigned>(s * KC * NWK * 4) : RSRC_OOB;
+    const unsigned slot = ring_base + static_cast<unsigned>((s % NS) * SWP * 4);
 #pragma unroll
-    for (int q = 0; q < LOADS; ++q)
-      dst[q] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                               r_bits, static_cast<int>(lo_q[q] + soff), 0, AUX_NT));
+    for (int q = 0; q < LOADS; ++q) load_lds16(r_bits, slot + 1024 * q, lo_q[q] + soff);
   };
   // only the first stage before the fold: a smaller burst of loads at kernel start, so
   // every wave's first stage (and the fold's inputs) arrive sooner; the rest of the
   // ring follows the fold
-  load_stage(s_begin, R[0]);
+  load_stage(s_begin);
 
   // ---- activation fold: xf = Hb_k(isc_scaled * su * x) / sqrt(block_in) as (x,x) pairs
   {
@@ -220,8 +247,12 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
       }
     }
   }
+  // Every load the compiler knows of (output scales, the fold's inputs) and stage s_begin
+  // have landed: a wait the compiler sees, so it puts none of its own (for a register a
+  // skipped fold chunk never read) after the next stages' loads, which it cannot count.
+  __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
 #pragma unroll
-  for (int b = 1; b < PF; ++b) load_stage(s_begin + b, R[b]);
+  for (int b = 1; b < NS; ++b) load_stage(s_begin + b);
   // No barrier: a wave decodes a stage as soon as the chunks it covers are folded for
   // every batch row (each wait ends: every wave publishes its chunks before it decodes
   // anything); once a wave has seen every chunk done it stops checking.
@@ -242,8 +273,9 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
   };
 
-  // ---- main loop: stage s is moved from registers to the wave's LDS buffer, the load
-  // of stage s + PF is issued into the freed registers, then stage s is decoded
+  // ---- main loop: wait for stage s (this wave's own loads: the NS - 1 stages issued after
+  // it may still be in flight), decode it from its ring slot, then refill that slot with
+  // stage s + NS
   const int r = lane & 15, gq = lane >> 4;
   const QuadPos qp = quad_pos_v<K, V>(r, gq);
   // B column r of the MFMA is batch row r (columns past the call's repeat its last row;
@@ -251,13 +283,13 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
   const uint32_t* xsr = xs + (NB > 1 ? min(r, nbv - 1) * XROW : 0);
   float4_t acc = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
   half8_t Bv[GEMV_G];
-  auto stage = [&](int s, u32x4_t (&src)[LOADS]) {
-    // lanes past the stage's last chunk write the buffer's padding: no masked region
-#pragma unroll
-    for (int q = 0; q < LOADS; ++q)
-      *reinterpret_cast<u32x4_t*>(mystg + 4 * (lane + 64 * q)) = src[q];
-    load_stage(s + PF, src);
+  auto stage = [&](int s) {
+    // loads complete in issue order: with stages s + 1 .. s + NS - 1 (LOADS each) issued
+    // after stage s, at most that many may be outstanding once stage s has landed
+    wait_vmcnt<(NS - 1) * LOADS>();
+    asm volatile("" ::: "memory");
     wait_chunks(s);
+    const uint32_t* mystg = myring + (s % NS) * SWP;
     const uint32_t* xst = xsr + s * KC * 16 + 4 * gq;
     // G tiles at a time: their LDS reads, then their decodes into separate A registers,
     // then their MFMAs on alternating accumulators, so a decode never waits for the
@@ -297,15 +329,18 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, acc, 0, 0, 0);
       }
     }
+    // every LDS read of the slot has returned before the next stage's loads write it
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    load_stage(s + NS);
   };
-  // PF stages per trip, all of them issued (a stage past s_end decodes nothing), so the
-  // register ring keeps a fixed shape. A SIMD issues from its oldest ready wave first, so
+  // A stage past s_end decodes nothing and its loads read nothing, so the number of loads
+  // in flight stays fixed for the waits. A SIMD issues from its oldest ready wave first, so
   // left alone its first wave finishes in about half the time of its last one, and the
   // last waves run alone, with nothing to hide their latencies behind. Each wave's issue
   // priority falls by one level per quarter of its stages done, so the waves of a SIMD
   // progress together (measured ~1 us less per 8B block, mostly on the gate+up launch).
   const int tot = s_end - s_begin > 0 ? s_end - s_begin : 1;
-  for (int s = s_begin; s < s_end; s += PF) {
+  for (int s = s_begin; s < s_end; ++s) {
     const int lvl = (4 * (s_end - s) - 1) / tot;
     if (lvl >= 3)
       __builtin_amdgcn_s_setprio(3);
@@ -315,8 +350,7 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
       __builtin_amdgcn_s_setprio(1);
     else
       __builtin_amdgcn_s_setprio(0);
-#pragma unroll
-    for (int b = 0; b < PF; ++b) stage(s + b, R[b]);
+    stage(s);
   }
   __builtin_amdgcn_s_setprio(0);
   // the ring's last loads (stages past the end) are not consumed: let them land

@@ -54,10 +54,12 @@ int launch_bfold(int cb, int nc, int nfold, const LinArgs& g, hipStream_t st) {
 template <int K, int CB, int V, int NB>
 static int launch_gemv_nb(int kc, const LinArgs& g, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(g.total));
+  // 16 rows: stages of 8 tiles (two 16-tile ring slots do not fit beside their activations)
+  constexpr int KC_WIDE = NB == 16 ? 8 : 16;
   if (kc == 8)
-    hipLaunchKernelGGL((gemv_kernel<K, CB, V, 8, GEMV_PF, NB>), grid, dim3(64 * GEMV_WAVES), 0, st, g);
+    hipLaunchKernelGGL((gemv_kernel<K, CB, V, 8, NB>), grid, dim3(64 * GEMV_WAVES), 0, st, g);
   else
-    hipLaunchKernelGGL((gemv_kernel<K, CB, V, 16, GEMV_PF, NB>), grid, dim3(64 * GEMV_WAVES), 0, st, g);
+    hipLaunchKernelGGL((gemv_kernel<K, CB, V, KC_WIDE, NB>), grid, dim3(64 * GEMV_WAVES), 0, st, g);
   return hipGetLastError() == hipSuccess ? 0 : 13;
 }
 
