@@ -33,13 +33,18 @@
 
 namespace trellis {
 
-// y[b0 + b] = sv * osc * Hb_n(t[b]) for the nbv batch columns staged in LDS as
-// t[b][TLS] (rows padded to TLS), summed over NR regions NR_OFF floats apart; one column
-// per wave at a time (WAVES waves).
-template <int CB, int WAVES, int TLS, int NR, int NR_OFF>
+// y[b0 + b] = sv * osc * Hb_n(t[b]) for the nbv <= NB batch columns staged in LDS as
+// t[b][TLS] (rows padded to TLS), summed over NR regions NR_OFF floats apart. Wave w folds
+// columns w, w + WAVES, ..: all of them at once, level by level (fwht_chunks), so their
+// lane exchanges overlap (one column after another, the fold of 64 columns measured ~2 us
+// at the end of every batched launch); a wave's slots past nbv repeat column nbv - 1 and
+// are not stored.
+template <int CB, int WAVES, int TLS, int NR, int NR_OFF, int NB>
 __device__ __forceinline__ void bg_out_fold(const LinArgs& g, const LinMat& m, const float* tl,
                                             int ob, int b0, int nbv, int rows) {
+  constexpr int C = (NB + WAVES - 1) / WAVES;   // columns per wave
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (wave >= nbv) return;
   const float nrm = m.nrm_out;
   float so[2];
 #pragma unroll
@@ -48,24 +53,33 @@ __device__ __forceinline__ void bg_out_fold(const LinArgs& g, const LinMat& m, c
     so[h] = m.sv[row] * m.osc[row] * nrm;
   }
   const FwhtLane fl = fwht_lane(lane, m.block_out);
-  for (int b = wave; b < nbv; b += WAVES) {
-    float lo = tl[b * TLS + lane], hi = tl[b * TLS + lane + 64];
+  float lo[C], hi[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int b = min(wave + WAVES * c, nbv - 1);
+    lo[c] = tl[b * TLS + lane];
+    hi[c] = tl[b * TLS + lane + 64];
     if (NR == 2) {
-      lo += tl[NR_OFF + b * TLS + lane];
-      hi += tl[NR_OFF + b * TLS + lane + 64];
+      lo[c] += tl[NR_OFF + b * TLS + lane];
+      hi[c] += tl[NR_OFF + b * TLS + lane + 64];
     }
-    if (lane >= rows) lo = 0.f;
-    if (lane + 64 >= rows) hi = 0.f;
+    if (lane >= rows) lo[c] = 0.f;
+    if (lane + 64 >= rows) hi[c] = 0.f;
     if (CB == CB_1MAD) {
-      lo = lo / 147.800537109375f;
-      hi = hi / 147.800537109375f;
+      lo[c] = lo[c] / 147.800537109375f;
+      hi[c] = hi[c] / 147.800537109375f;
     }
-    fwht_chunk(lo, hi, m.block_out, lane, fl);
+  }
+  fwht_chunks<C>(lo, hi, m.block_out, lane, fl);
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int b = wave + WAVES * c;
+    if (b >= nbv) break;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int rl = lane + 64 * h;
       if (rl < rows) {
-        const float v = (h ? hi : lo) * so[h];
+        const float v = (h ? hi[c] : lo[c]) * so[h];
         const long long o = static_cast<long long>(b0 + b) * m.ldy + ob * 128 + rl;
         if (g.y_f16)
           static_cast<_Float16*>(m.y)[o] = static_cast<_Float16>(v);
@@ -283,7 +297,7 @@ __global__ __launch_bounds__(64 * BG_WAVES) void bgemm_kernel(LinArgs g) {
     }
     return;
   }
-  bg_out_fold<CB, BG_WAVES, TLS, NR, NR_OFF>(g, m, tl, ob, b0, nbv, rows);
+  bg_out_fold<CB, BG_WAVES, TLS, NR, NR_OFF, NB>(g, m, tl, ob, b0, nbv, rows);
 }
 
 // Split-K reduction of bgemm_kernel: one wave per (matrix, 128-row block, batch column):
@@ -306,6 +320,13 @@ __global__ __launch_bounds__(256) void bfold_kernel(LinArgs g) {
   if (n >= nbv) return;
   const int rows = min(128, m.n - ob * 128);
   const int S = m.S;
+  // the output scales first: their loads are in flight with the partial sums'
+  float so[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int row = ob * 128 + min(lane + 64 * h, rows - 1);
+    so[h] = m.sv[row] * m.osc[row];
+  }
   const float* p = m.part + static_cast<size_t>(ob * ncb + cb) * S * NB * 128 + n * 128;
   float lo = 0.f, hi = 0.f;
   for (int s0 = 0; s0 < S; s0 += 8) {
@@ -334,7 +355,7 @@ __global__ __launch_bounds__(256) void bfold_kernel(LinArgs g) {
     const int rl = lane + 64 * h;
     if (rl < rows) {
       const int row = ob * 128 + rl;
-      const float v = (h ? hi : lo) * (m.sv[row] * m.osc[row] * nrm);
+      const float v = (h ? hi : lo) * (so[h] * nrm);
       const long long o = static_cast<long long>(b0 + n) * m.ldy + row;
       if (g.y_f16)
         static_cast<_Float16*>(m.y)[o] = static_cast<_Float16>(v);

@@ -75,6 +75,13 @@ __device__ __forceinline__ unsigned lds_addr(const void* p) {
       (__attribute__((address_space(3))) void*)(const_cast<void*>(p))));
 }
 
+// s_waitcnt for the vector-memory counter only (expcnt and lgkmcnt at their maxima)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 // One 16-byte global -> LDS load per lane (gfx950 buffer_load_dwordx4 ... lds, nontemporal):
 // the 16 bytes at byte offset `voff` of the buffer (zeros past its end) land at LDS byte
 // address `lds_base` + 16 * lane; lds_base is wave-uniform (it goes to M0, which is saved
@@ -222,6 +229,44 @@ __device__ __forceinline__ void fwht_chunk(float& lo, float& hi, int B, int lane
   fwht_chunk(lo, hi, B, lane, fwht_lane(lane, B));
 }
 
+// fwht_chunk on C independent chunks, level by level, so the chunks' dependent lane
+// exchanges overlap instead of running one chunk after another (same operations per chunk,
+// same results).
+template <int C>
+__device__ __forceinline__ void fwht_chunks(float (&lo)[C], float (&hi)[C], int B, int lane,
+                                            const FwhtLane& fl) {
+  if (B > 1)
+#pragma unroll
+    for (int c = 0; c < C; ++c) butterfly<1>(lo[c], hi[c], fl.s1, lane);
+  if (B > 2)
+#pragma unroll
+    for (int c = 0; c < C; ++c) butterfly<2>(lo[c], hi[c], fl.s2, lane);
+  if (B > 4)
+#pragma unroll
+    for (int c = 0; c < C; ++c) butterfly<4>(lo[c], hi[c], fl.s4, lane);
+  if (B > 8)
+#pragma unroll
+    for (int c = 0; c < C; ++c) butterfly<8>(lo[c], hi[c], fl.s8, lane);
+  if (B > 16)
+#pragma unroll
+    for (int c = 0; c < C; ++c) butterfly_swap<16>(lo[c], hi[c]);
+  if (B > 32)
+#pragma unroll
+    for (int c = 0; c < C; ++c) butterfly_swap<32>(lo[c], hi[c]);
+  if (B == 128)
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const float a = lo[c], b = hi[c];
+      lo[c] = a + b;
+      hi[c] = a - b;
+    }
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    lo[c] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, lo[c]) ^ fl.flip);
+    hi[c] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, hi[c]) ^ fl.flip);
+  }
+}
+
 __device__ __forceinline__ uint32_t dup_half(float v) {
   const _Float16 h = static_cast<_Float16>(v);
   const uint16_t u = __builtin_bit_cast(uint16_t, h);
@@ -254,11 +299,12 @@ __device__ __forceinline__ int xf_pair_slot(int e) {
 
 // ---------------------------------------------------------------- x fold
 // xf = Hb_k(isc * su * x) scaled by 1/sqrt(block_in), stored as (x,x) fp16 pairs. One
-// wave per (matrix, 4 batch rows, 128-column chunk): su * isc of the chunk is loaded once
-// for the 4 rows, every load is a range-checked buffer load issued up front (rows past the
-// call's read zeros), and the four transforms run back to back. Defined in one
-// translation unit only.
-constexpr int XFOLD_ROWS = 4;
+// wave per (matrix, batch row, 128-column chunk), every load a range-checked buffer load
+// issued up front. The kernel is latency-bound (a few MB at most): one row per wave gives
+// every SIMD several waves to overlap the transform's dependent lane exchanges (8B gate+up
+// fold at batch 64, alone in a graph chain: 2.7 us per launch, against 2.9 with 2 rows and
+// 3.6 with 4 rows per wave). Defined in one translation unit only.
+constexpr int XFOLD_ROWS = 1;
 #ifdef TRELLIS_XFOLD_DEFINE
 __global__ __launch_bounds__(256) void xfold_kernel(LinArgs g) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;

@@ -80,13 +80,6 @@ __host__ __device__ constexpr int gemv_lds_bytes(int K, int KC, int nb) {
               gemv_kr_max(nb) / 8 + 4);
 }
 
-// s_waitcnt for the vector-memory counter only (expcnt and lgkmcnt at their maxima)
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
 template <int K, int CB, int V, int KC, int NB>
 __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
   constexpr int NWK = 8 * K;                 // words per tile
@@ -440,8 +433,8 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
   if (wave != 0) return;
 
   // ---- wave 0: the two k-halves, then (split-K) publish, ticket, and in the last
-  // workgroup of the block the partials in slice order; then y = sv * osc * Hb_n(t), one
-  // batch row at a time
+  // workgroup of the block the partials in slice order; then y = sv * osc * Hb_n(t) of
+  // every batch row
   float t0[NB], t1[NB];
 #pragma unroll
   for (int n = 0; n < NB; ++n) {
@@ -500,15 +493,20 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
   }
   const float nrm = m.nrm_out;
   const FwhtLane fl = fwht_lane(lane, m.block_out);
+  // every row's transform at once (rows past the call's hold a copy of a valid row's sums
+  // and are not stored), so their lane exchanges overlap
+  if (CB == CB_1MAD) {
+#pragma unroll
+    for (int n = 0; n < NB; ++n) {
+      t0[n] = t0[n] / 147.800537109375f;
+      t1[n] = t1[n] / 147.800537109375f;
+    }
+  }
+  fwht_chunks<NB>(t0, t1, m.block_out, lane, fl);
 #pragma unroll
   for (int n = 0; n < NB; ++n) {
     if (n >= nbv) break;
-    float a = t0[n], b = t1[n];
-    if (CB == CB_1MAD) {
-      a = a / 147.800537109375f;
-      b = b / 147.800537109375f;
-    }
-    fwht_chunk(a, b, m.block_out, lane, fl);
+    const float a = t0[n], b = t1[n];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int rl = lane + 64 * h;
