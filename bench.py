@@ -107,9 +107,10 @@ def capture(torch, fn):
 
 
 def run_block(te, torch, dev, layers, groups, B, K, V, steps, warmup, min_bytes=1.0e9,
-              per_launch=True, mma_f16=False, copies=None):
+              per_launch=True, mma_f16=False, copies=None, singles=True):
     """Time `steps` replays of the block (its launches in order) over distinct weight copies.
-    Returns (seconds per step, {group: us per launch}, {layer: us per launch})."""
+    Returns (seconds per step, {group: us per launch}, {layer: us per launch}); singles=False
+    never launches the layers one by one (a counter run then sees only the group launches)."""
     block_bytes = sum(n * k * K // 8 for _, n, k in layers)
     if copies is None:
         copies = max(2, math.ceil(min_bytes / block_bytes))
@@ -133,8 +134,9 @@ def run_block(te, torch, dev, layers, groups, B, K, V, steps, warmup, min_bytes=
 
     for c in range(copies):            # allocates every workspace once, before capture
         step(c)
-        for name, _, _ in layers:
-            single(c, name)
+        if singles:
+            for name, _, _ in layers:
+                single(c, name)
     torch.cuda.synchronize()
     graphs = [capture(torch, lambda c=c: step(c)) for c in range(copies)]
     for s in range(warmup):
@@ -167,8 +169,9 @@ def run_block(te, torch, dev, layers, groups, B, K, V, steps, warmup, min_bytes=
 
         us_group = {gname: round(per_launch_us(lambda c, gname=gname: step(c, gname)), 3)
                     for gname, _ in groups}
-        us_layer = {name: round(per_launch_us(lambda c, name=name: single(c, name)), 3)
-                    for name, _, _ in layers}
+        if singles:
+            us_layer = {name: round(per_launch_us(lambda c, name=name: single(c, name)), 3)
+                        for name, _, _ in layers}
     del graphs, grps, blocks
     torch.cuda.empty_cache()
     return sec, us_group, us_layer, copies
@@ -419,6 +422,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the LM-head GEMV and embedding-row lookup figures")
+    ap.add_argument("--no-single", action="store_true",
+                    help="skip the one-layer-per-launch figures (for counter runs: the group "
+                         "launches are then the only ones of their grid sizes)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -436,7 +442,8 @@ def main():
     log(f"[bench] block batch {B} K={K} V={V}")
     sec, us_group, us_layer, copies = run_block(te, torch, dev, LAYERS, GROUPS, B, K, V,
                                                 args.steps, args.warmup, mma_f16=args.mma_f16,
-                                                copies=args.weight_copies)
+                                                copies=args.weight_copies,
+                                                singles=not args.no_single)
     gbs = block_bytes / sec / 1e9
     dom_us = us_group[DOMINANT]
     dom_bytes = 2 * 12288 * 4096 * K // 8
