@@ -218,16 +218,29 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
       if (ch < nch && f_r1 > f_r0) {
         const int e0 = ch * 128 + lane, e1 = e0 + 64;
         // columns past the k-range loaded as zeros; an f16 row stride is even, so the
-        // element's half within its word follows e
+        // element's half within its word follows e. Rows are transformed RG at a time,
+        // level by level (fwht_chunks), so their dependent lane exchanges overlap (one row
+        // after another, a wave's 16-row fold took up to ~6 us at batch 16); a group's rows
+        // that are not this wave's were loaded as zeros and are not stored.
+        constexpr int RG = NB < 8 ? NB : 8;
 #pragma unroll
-        for (int n = 0; n < NB; ++n) {
-          if (n >= f_r1) break;              // rows past the call's are never read
-          if (n < f_r0) continue;
-          float lo = act_value(fw[f][n][0], e0, g.x_f16) * (fsu[f][0] * fis[f][0]);
-          float hi = act_value(fw[f][n][1], e1, g.x_f16) * (fsu[f][1] * fis[f][1]);
-          fwht_chunk(lo, hi, m.block_in, lane, fl);
-          xs[n * XROW + e0] = dup_half(lo * nrm);
-          xs[n * XROW + e1] = dup_half(hi * nrm);
+        for (int g0 = 0; g0 < NB; g0 += RG) {
+          if (g0 >= f_r1 || g0 + RG <= f_r0) continue;
+          float lo[RG], hi[RG];
+#pragma unroll
+          for (int j = 0; j < RG; ++j) {
+            lo[j] = act_value(fw[f][g0 + j][0], e0, g.x_f16) * (fsu[f][0] * fis[f][0]);
+            hi[j] = act_value(fw[f][g0 + j][1], e1, g.x_f16) * (fsu[f][1] * fis[f][1]);
+          }
+          fwht_chunks<RG>(lo, hi, m.block_in, lane, fl);
+#pragma unroll
+          for (int j = 0; j < RG; ++j) {
+            const int n = g0 + j;
+            if (n >= f_r0 && n < f_r1) {
+              xs[n * XROW + e0] = dup_half(lo[j] * nrm);
+              xs[n * XROW + e1] = dup_half(hi[j] * nrm);
+            }
+          }
         }
         // publish the chunk's rows: their xs words are written before the count
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
