@@ -249,14 +249,24 @@ __global__ __launch_bounds__(64 * BG_WAVES) void bgemm_kernel(LinArgs g) {
             if (st * KT + j < ntl) {
               const uint32_t* t0 = mystg + t * NWK;
               const uint32_t* t1 = mystg + (TPL + t) * NWK;
-              const half8_t A0 = decode_a<K, CB, V>(t0[qp.wa], t0[qp.wb], qp.sh);
-              const half8_t A1 = decode_a<K, CB, V>(t1[qp.wa], t1[qp.wb], qp.sh);
+              // every LDS read of the tile (window words, the NC B fragments) before the
+              // decode, so the fragments' latency hides behind it (read just before each
+              // MFMA pair, it was exposed)
+              const uint32_t w0a = t0[qp.wa], w0b = t0[qp.wb], w1a = t1[qp.wa], w1b = t1[qp.wb];
+              half8_t Bf[NC];
+#pragma unroll
+              for (int c = 0; c < NC; ++c)
+                Bf[c] = __builtin_bit_cast(half8_t, *reinterpret_cast<const u32x4_t*>(xb + c * 16 * XW + j * 16));
+              // no instruction crosses this point (the scheduler would otherwise sink each
+              // fragment's read back in front of its MFMAs); with 8 chunks the fragments'
+              // registers would spill
+              if constexpr (NC <= 4) __builtin_amdgcn_sched_barrier(0);
+              const half8_t A0 = decode_a<K, CB, V>(w0a, w0b, qp.sh);
+              const half8_t A1 = decode_a<K, CB, V>(w1a, w1b, qp.sh);
 #pragma unroll
               for (int c = 0; c < NC; ++c) {
-                const half8_t B = __builtin_bit_cast(
-                    half8_t, *reinterpret_cast<const u32x4_t*>(xb + c * 16 * XW + j * 16));
-                acc[0][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, B, acc[0][c], 0, 0, 0);
-                acc[1][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, B, acc[1][c], 0, 0, 0);
+                acc[0][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, Bf[c], acc[0][c], 0, 0, 0);
+                acc[1][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, Bf[c], acc[1][c], 0, 0, 0);
               }
             }
           }
