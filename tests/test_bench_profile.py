@@ -1,0 +1,38 @@
+"""The committed counter summary that bench.py's roofline.traffic reads: it parses, and the
+scaled bytes per gate+up launch agree with the algorithmic bytes (2 x 12288 x 4096 packed
+K=3 words), so the figure can neither vanish (a key renamed) nor drift below the bytes the
+kernel must read (a wrong calibration pass)."""
+import os
+import sys
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, ROOT)
+
+import bench  # noqa: E402
+
+ALGORITHMIC = 2 * 12288 * 4096 * 3 // 8
+
+
+def test_traffic_profile_parses_and_covers_the_packed_bytes():
+    t = bench.traffic_from_profile()
+    assert t is not None, "profiles/gemv_gate_up_b1_traffic.txt missing a key bench.py reads"
+    # every packed word once, plus activations, scales and fold inputs: a few percent more
+    assert 1.0 <= t / ALGORITHMIC <= 1.1, t / ALGORITHMIC
+
+
+def test_dram_counters_agree_with_the_scaled_fetch():
+    vals = {}
+    for line in open(bench.TRAFFIC_FILE):
+        parts = line.split()
+        if len(parts) == 2 and not line.startswith("#"):
+            vals[parts[0]] = float(parts[1])
+    # the DRAM request counters need no scale (the 1 GiB calibration sum reads 1 GiB by them)
+    assert abs(vals["cal_read_dram_kib"] / vals["cal_kib"] - 1.0) < 0.01
+    dram = vals["dram_read_kib"] * 1024
+    assert 1.0 <= dram / ALGORITHMIC <= 1.1
+    scaled = vals["fetch_kib"] * vals["cal_kib"] / vals["cal_read_fetch_kib"] * 1024
+    assert abs(scaled / dram - 1.0) < 0.05
+
+
+def test_traffic_absent_file_is_none(tmp_path):
+    assert bench.traffic_from_profile(str(tmp_path / "missing.txt")) is None
