@@ -17,6 +17,12 @@ restatement of the reference decode+restore+matmul (oracle/torch_cpu.py) on a bo
 sample, per configuration and layer. The bit-rate sweep (configs[4]: K=2,3,4 x V=1,2 on
 the 8B gate/up/down shapes, at batch 1 and at a 512-token prefill) runs by default
 (--no-sweep skips it), each point with its own roofline.
+
+The CPU-baseline leg also checks what the timed launches computed: after each timed run,
+copy 0's graph is replayed once more and sampled 128-row output blocks are copied to the
+host (three per layer, one per layer at a sweep point); the oracle's float64 W_hat @ x
+judges them at the reference's 1e-3 metric ("output_check"). A failed check prints the
+JSON line and exits with status 3. --no-cpu-baseline skips both.
 """
 from __future__ import annotations
 
@@ -106,11 +112,39 @@ def capture(torch, fn):
     return g
 
 
+def take_samples(blk, xs, ys, layers, label, per_layer):
+    """Host copies for the output check of one timed run: per layer, the packed words of
+    `per_layer` 128-row output blocks (first, middle, last) of one weight copy with its
+    metadata, the input rows and the outputs that copy's timed launches wrote. A 128-row
+    block of y depends only on its own 8 bands (the out-dim Hadamard block is 128)."""
+    out = []
+    for name, n, k in layers:
+        lin = blk[name]
+        tin, nb = k // 16, n // 128
+        obs = sorted({0, nb // 2, nb - 1}) if per_layer >= 3 else [nb - 1]
+        B = xs[name].shape[0]
+        # every batch row up to 64; above, 32 rows spread over the batch (first and last)
+        rows = list(range(B)) if B <= 64 else sorted({round(i * (B - 1) / 31) for i in range(32)})
+        y = ys[name][rows]
+        out.append({
+            "run": label, "layer": name, "n": n, "k": k, "K": lin.K, "V": lin.V,
+            "codebook": lin.codebook, "scale": lin.scale,
+            "su": lin.su.cpu().numpy(), "sv": lin.sv.cpu().numpy(),
+            "isc_scaled": lin.isc_scaled.cpu().numpy(), "osc": lin.osc.cpu().numpy(),
+            "x": xs[name][rows].float().cpu().numpy(),
+            "blocks": [(ob, lin.bits[ob * 8 * tin:(ob + 1) * 8 * tin].cpu().numpy().view("uint32"),
+                        y[:, ob * 128:(ob + 1) * 128].cpu().numpy()) for ob in obs]})
+    return out
+
+
 def run_block(te, torch, dev, layers, groups, B, K, V, steps, warmup, min_bytes=1.0e9,
-              per_launch=True, mma_f16=False, copies=None, singles=True):
+              per_launch=True, mma_f16=False, copies=None, singles=True, samples=None,
+              label="", sample_blocks=3):
     """Time `steps` replays of the block (its launches in order) over distinct weight copies.
     Returns (seconds per step, {group: us per launch}, {layer: us per launch}); singles=False
-    never launches the layers one by one (a counter run then sees only the group launches)."""
+    never launches the layers one by one (a counter run then sees only the group launches).
+    With a `samples` list, copy 0's graph is replayed once more after the timed steps and
+    what its launches wrote is appended for the output check (take_samples)."""
     block_bytes = sum(n * k * K // 8 for _, n, k in layers)
     if copies is None:
         copies = max(2, math.ceil(min_bytes / block_bytes))
@@ -147,6 +181,10 @@ def run_block(te, torch, dev, layers, groups, B, K, V, steps, warmup, min_bytes=
         graphs[s % copies].replay()
     torch.cuda.synchronize()
     sec = (time.perf_counter() - t0) / steps
+    if samples is not None:
+        graphs[0].replay()
+        torch.cuda.synchronize()
+        samples.extend(take_samples(blocks[0], xs, ys, layers, label, sample_blocks))
 
     us_group, us_layer = {}, {}
     if per_launch:
@@ -262,6 +300,48 @@ def cpu_baseline(budget_s: float = 30.0):
                              f"on {cores} threads: {enc_s:.2f} s"}
 
 
+OUTPUT_TOL = 1e-3   # validate_packed_linear.py:66-69: max|y - y_ref| / max|y_ref|
+
+
+def check_outputs(samples, tol=OUTPUT_TOL):
+    """Part of the CPU-baseline leg: every sampled 128-row output block of every timed run
+    (take_samples) against the oracle's float64 W_hat @ x (oracle/trellis_np.py
+    packed_linear_ref: decode, then the restore of qtip.py:262-268), by the metric of
+    validate_packed_linear.py:66-69. The bench's layers fold an fp16 scale into fp16 input
+    scales (isc_scaled = f32(isc) * scale, packed.js:51-52); that product is exact in f32,
+    so isc is recovered exactly and the oracle sees the stored record."""
+    import numpy as np
+    from concurrent.futures import ThreadPoolExecutor
+    from oracle import trellis_np as tn
+
+    def one(job):
+        s, ob, bits, y = job
+        scale = np.float32(s["scale"])
+        isc = (s["isc_scaled"] / scale).astype(np.float16)
+        if not np.array_equal(isc.astype(np.float32) * scale, s["isc_scaled"]):
+            raise ValueError(f"{s['run']} {s['layer']}: isc_scaled is not f32(fp16 isc) * scale")
+        sl = slice(ob * 128, ob * 128 + 128)
+        rec = tn.IPRecord(128, s["k"], s["K"], s["su"], s["sv"][sl], isc, s["osc"][sl], scale,
+                          codebook=s["codebook"], V=s["V"])
+        return tn.rel_err(y, tn.packed_linear_ref(bits, rec, s["x"]))
+
+    jobs = [(s, ob, bits, y) for s in samples for ob, bits, y in s["blocks"]]
+    t0 = time.perf_counter()
+    with ThreadPoolExecutor(max_workers=min(8, len(os.sched_getaffinity(0)))) as ex:
+        errs = list(ex.map(one, jobs))
+    worst = max(range(len(jobs)), key=lambda i: errs[i]) if jobs else None
+    bad = [f"{s['run']} {s['layer']} rows {ob * 128}+128: {e:.3g}"
+           for (s, ob, _, _), e in zip(jobs, errs) if not e < tol]
+    res = {"ok": not bad, "tol": tol, "metric": "max|y - y_oracle| / max|y_oracle| per block",
+           "runs": len({s["run"] for s in samples}), "blocks_checked": len(jobs),
+           "max_rel_err": float(f"{max(errs):.3g}") if errs else None,
+           "worst": (f"{jobs[worst][0]['run']} {jobs[worst][0]['layer']} rows "
+                     f"{jobs[worst][1] * 128}+128") if jobs else None,
+           "failures": bad[:10], "seconds": round(time.perf_counter() - t0, 1)}
+    log(f"[bench] output check: {res}")
+    return res
+
+
 def extras(te, torch, dev, steps, K=4):
     """Next-row measurements on a Qwen3-8B vocab matrix (151936 x 4096, K=4, as the 8B export
     quantizes the LM head): the batch-1 LM-head GEMV, and embedding-row lookups
@@ -322,14 +402,14 @@ def block_flops(layers, B):
     return sum(2 * B * n * k for _, n, k in layers)
 
 
-def batched_figure(te, torch, dev, bs, K, V, args):
+def batched_figure(te, torch, dev, bs, K, V, args, samples=None):
     """The block at batch `bs` through the batched MFMA path (x fold, decode-to-MFMA GEMM,
     split-K fold), exact and in the fp16-weight mode, with the gate+up launch's fp16 MFMA
     roofline (algorithmic 2*bs*n*k flops over the launch, launch gap included)."""
     log(f"[bench] block batch {bs}")
     steps, warmup = max(20, args.steps // 10), max(3, args.warmup // 5)
     sec, grp, _, _ = run_block(te, torch, dev, LAYERS, GROUPS, bs, K, V, steps, warmup,
-                               per_launch=True)
+                               per_launch=True, samples=samples, label=f"block batch {bs}")
     fl = block_flops(LAYERS, bs)
     dom_fl = 2 * bs * 2 * 12288 * 4096
     dom_tf = dom_fl / (grp[DOMINANT] * 1e-6) / 1e12
@@ -349,7 +429,8 @@ def batched_figure(te, torch, dev, bs, K, V, args):
     # the same block with the fp16-weight MFMA mode (each codebook value rounded once
     # to fp16, one MAC per weight; max rel err ~2-3e-4 against the exact default)
     sech, grph, _, _ = run_block(te, torch, dev, LAYERS, GROUPS, bs, K, V, steps, warmup,
-                                 per_launch=True, mma_f16=True)
+                                 per_launch=True, mma_f16=True, samples=samples,
+                                 label=f"block batch {bs} fp16-weight mode")
     out["mma_f16"] = {"us_per_block": round(sech * 1e6, 2),
                       "tflops": round(fl / sech / 1e12, 2),
                       "mfma_frac_of_fp16_peak": round(fl / sech / 1e12 / MFMA_FP16_PEAK_TFLOPS, 4),
@@ -360,7 +441,7 @@ def batched_figure(te, torch, dev, bs, K, V, args):
     return out
 
 
-def sweep_point(te, torch, dev, K, V, B, args):
+def sweep_point(te, torch, dev, K, V, B, args, samples=None):
     """One point of the bit-rate sweep: gate, up and down of the 8B block, one launch each,
     at K bits, V weights per step and batch B (1, or a 512-token prefill), over >= 1 GB of
     distinct weight copies. Roofline of the whole point: HBM on the packed bytes at batch 1,
@@ -368,7 +449,8 @@ def sweep_point(te, torch, dev, K, V, B, args):
     log(f"[bench] sweep K={K} V={V} batch={B}")
     steps = max(20, args.steps) if B == 1 else 10
     sec, sg, _, copies = run_block(te, torch, dev, MLP, [(n, (n,)) for n, _, _ in MLP], B, K, V,
-                                   steps, 3, per_launch=True)
+                                   steps, 3, per_launch=True, samples=samples,
+                                   label=f"sweep K={K} V={V} batch {B}", sample_blocks=1)
     pb = sum(n * k * K // 8 for _, n, k in MLP)
     fl = block_flops(MLP, B)
     gbs, tfl = pb / sec / 1e9, fl / sec / 1e12
@@ -439,11 +521,15 @@ def main():
     B, K, V = args.batch, args.K, args.V
     block_bytes = sum(n * k * K // 8 for _, n, k in LAYERS)
 
+    # host copies of sampled output blocks of every timed run, checked against the oracle
+    # in the CPU-baseline leg (check_outputs)
+    samples = None if args.no_cpu_baseline else []
     log(f"[bench] block batch {B} K={K} V={V}")
     sec, us_group, us_layer, copies = run_block(te, torch, dev, LAYERS, GROUPS, B, K, V,
                                                 args.steps, args.warmup, mma_f16=args.mma_f16,
                                                 copies=args.weight_copies,
-                                                singles=not args.no_single)
+                                                singles=not args.no_single, samples=samples,
+                                                label=f"block batch {B}")
     gbs = block_bytes / sec / 1e9
     dom_us = us_group[DOMINANT]
     dom_bytes = 2 * 12288 * 4096 * K // 8
@@ -453,12 +539,12 @@ def main():
     batched = {}
     if not args.no_batch64 and B == 1:
         for bs in (16, 64):
-            batched[bs] = batched_figure(te, torch, dev, bs, K, V, args)
+            batched[bs] = batched_figure(te, torch, dev, bs, K, V, args, samples)
     batch64 = batched.get(64)
 
     sweep = None
     if not args.no_sweep and B == 1:
-        sweep = [sweep_point(te, torch, dev, Ks, Vs, Bs, args)
+        sweep = [sweep_point(te, torch, dev, Ks, Vs, Bs, args, samples)
                  for Ks in (2, 3, 4) for Vs in (1, 2) for Bs in (1, 512)]
 
     extra = None
@@ -470,7 +556,8 @@ def main():
         for bs in (2, 4, 8):
             ssec_b, _, _, _ = run_block(te, torch, dev, LAYERS, GROUPS, bs, K, V,
                                         max(20, args.steps // 5), max(3, args.warmup // 5),
-                                        per_launch=False)
+                                        per_launch=False, samples=samples,
+                                        label=f"block batch {bs}")
             small[str(bs)] = round(ssec_b * 1e6, 2)
         extra["us_per_block_small_batch"] = small
         log(f"[bench] extras {extra}")
@@ -521,7 +608,11 @@ def main():
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline")
         out["cpu_baseline"] = cpu_baseline()
+        out["output_check"] = check_outputs(samples)
     print(json.dumps(out), flush=True)
+    if not out.get("output_check", {"ok": True})["ok"]:
+        log("[bench] OUTPUT CHECK FAILED: the timed launches do not match the oracle")
+        sys.exit(3)
 
 
 if __name__ == "__main__":
