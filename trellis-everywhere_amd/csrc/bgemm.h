@@ -3,14 +3,15 @@
 //
 // A workgroup of 16 waves owns one 128-row output block (the out-dim Hadamard block) x
 // NB = 16*NC batch columns x one k-range of `kr` tile columns, walked in steps of KT tiles
-// (8, or 4 at 128 columns). Wave w = (band pair bp = w % 4, k-lane kl = w / 4): the four
-// waves of a SIMD share band pair bp (bands 2bp, 2bp+1) and split every step's tiles
-// between them (tile j of a step belongs to k-lane j % 4), so a SIMD always has four
+// (16 at 16 columns, 8, or 4 at 128 columns). Wave w = (band group bg = w % NG, k-lane
+// kl = w / NG), a band group being BW = 2 or 4 adjacent bands (NG = 8 / BW groups, KL =
+// 16 / NG k-lanes): the waves of a SIMD share a band group and split every step's tiles
+// between them (tile j of a step belongs to k-lane j % KL), so a SIMD always has four
 // waves to switch between:
 //   * the B tile of a step (xf[batch cols][KT*16] as (x, x) fp16 pairs written by
 //     xfold_kernel) is loaded two steps ahead into registers by all 1024 threads, stored
 //     to one half of a double-buffered LDS area, and read by every wave: each fragment
-//     serves the 2 bands of each of the 4 band pairs; one barrier per step;
+//     serves the BW bands of each of the NG band groups; one barrier per step;
 //   * each wave's packed words ride a two-step register ring and a wave-private LDS
 //     buffer (for the lanes' window reads), as in gemv_kernel;
 //   * each wave decodes a tile of each of its bands once, straight into the A operand of
@@ -21,7 +22,7 @@
 //   * the B rows are padded by 8 words (a row stride of 8 mod 64 words): the 16 batch
 //     rows x 4 column groups of a fragment read then run at the LDS's full rate on gfx950
 //     (measured 177 B/clk per CU, against 115 with a 4-word pad, whose rows collide);
-//   * the epilogue adds the four k-lanes' sums into t[NB][128] in LDS in k-lane order
+//   * the epilogue adds the KL k-lanes' sums into t[NB][128] in LDS in k-lane order
 //     (deterministic); with one k-range the workgroup applies y = sv * osc * Hb_n(t)
 //     itself, otherwise it stores its partial block and bfold_kernel (next launch) adds
 //     the slices in slice order and folds, one wave per batch column: reducing inside the
@@ -97,15 +98,26 @@ template <int NC, int F16> struct BgStep {
   static constexpr int KT = F16 ? 8 : NC == 1 ? 16 : NC <= 4 ? 8 : 4;
 };
 constexpr int BG_WAVES = 16;
-constexpr int BG_KL = 4;   // k-lanes: waves of one band pair splitting each step's tiles
+// bands per wave: 4 at 16 batch columns (8 k-lanes: each B fragment read from LDS feeds 4
+// bands instead of 2; the 8B gate+up group at batch 16 27.8 -> 26.6-27.1 us), otherwise 2
+// (a band pair, 4 k-lanes: at 32 and 64 columns 4 bands measured no faster on gate+up and
+// 4-6 % slower on the split-K launches, whose epilogue adds twice the k-lanes); the k-step
+// must hold a tile column per k-lane
+template <int NC, int F16> struct BgBands {
+  static constexpr int BW = (!F16 && NC == 1) ? 4 : 2;
+};
 
 template <int K, int CB, int V, int NC, int F16>
 __global__ __launch_bounds__(64 * BG_WAVES) void bgemm_kernel(LinArgs g) {
   constexpr int NWK = 8 * K;
   constexpr int KT = BgStep<NC, F16>::KT;          // tile columns per k-step
-  // tiles per band per k-lane per step: exact mode, tiles kl, kl + 4, ...; fp16-weight
+  constexpr int BW = BgBands<NC, F16>::BW;         // bands per wave
+  constexpr int NG = 8 / BW;                       // band groups of the block
+  constexpr int KL = BG_WAVES / NG;                // k-lanes: waves of one band group
+  // tiles per band per k-lane per step: exact mode, tiles kl, kl + KL, ...; fp16-weight
   // mode, the tile pair 2kl, 2kl + 1 (one MFMA per pair)
-  constexpr int TPL = F16 ? 2 : KT / BG_KL;
+  constexpr int TPL = F16 ? 2 : KT / KL;
+  static_assert(F16 || (KT % KL == 0 && TPL >= 1), "a tile column per k-lane per step");
   constexpr int WPT = F16 ? 8 : 16;                // B words per tile column and batch row
   constexpr int XW = KT * WPT + 8;                 // LDS words per B row (+8: bank spread)
   constexpr int NB = 16 * NC;                      // batch columns per workgroup
@@ -114,11 +126,11 @@ __global__ __launch_bounds__(64 * BG_WAVES) void bgemm_kernel(LinArgs g) {
   constexpr int XLOADS = (XCH + 64 * BG_WAVES - 1) / (64 * BG_WAVES);
   constexpr int XBUF = NB * XW;                    // words per B buffer
   constexpr int CPT = NWK / 4;                     // 16-byte chunks per tile
-  constexpr int BCH = 2 * TPL * CPT;               // 16-byte chunks per wave per step
+  constexpr int BCH = BW * TPL * CPT;              // 16-byte chunks per wave per step
   constexpr int BLOADS = (BCH + 63) / 64;
   constexpr int BSW = BLOADS * 256;                // words per wave buffer: every lane's chunks
   static_assert(NB * 136 <= 2 * XBUF, "epilogue t[NB][136] reuses the B buffers");
-  static_assert(!F16 || KT == 2 * BG_KL, "fp16-weight mode: one tile pair per k-lane per step");
+  static_assert(!F16 || (KT == 2 * KL && BW == 2), "fp16-weight mode: one tile pair per k-lane per step");
   __shared__ __align__(16) uint32_t xsb[2 * XBUF];
   __shared__ __align__(16) uint32_t bst[BG_WAVES * BSW];
   // epilogue: t[NB][TLS] (rows padded like the B rows, so a fragment's float4 writes
@@ -129,7 +141,7 @@ __global__ __launch_bounds__(64 * BG_WAVES) void bgemm_kernel(LinArgs g) {
   float* tl = reinterpret_cast<float*>(xsb);
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int bp = wave & 3, kl = wave >> 2;
+  const int bg = wave % NG, kl = wave / NG;
   const int mi = locate_mat(g, blockIdx.x, false);
   const LinMat& m = g.m[mi];
   const int local = blockIdx.x - m.item0;
@@ -167,8 +179,8 @@ __global__ __launch_bounds__(64 * BG_WAVES) void bgemm_kernel(LinArgs g) {
     const int ch = lane + 64 * q;
     const int bb = ch / (TPL * CPT), rem = ch % (TPL * CPT);
     const int t = rem / CPT, c = rem % CPT;
-    const int tile = c0 + (F16 ? 2 * kl + t : kl + BG_KL * t);
-    boff[q] = ch < BCH ? static_cast<unsigned>(((2 * bp + bb) * m.tiles_in + tile) * NWK * 4 + c * 16)
+    const int tile = c0 + (F16 ? 2 * kl + t : kl + KL * t);
+    boff[q] = ch < BCH ? static_cast<unsigned>(((BW * bg + bb) * m.tiles_in + tile) * NWK * 4 + c * 16)
                        : RSRC_OOB;
   }
   u32x4_t xr[2][XLOADS], br[2][BLOADS];
@@ -196,9 +208,9 @@ __global__ __launch_bounds__(64 * BG_WAVES) void bgemm_kernel(LinArgs g) {
 
   const int r = lane & 15, gq = lane >> 4;
   const QuadPos qp = quad_pos_v<K, V>(r, gq);
-  float4_t acc[2][NC];
+  float4_t acc[BW][NC];
 #pragma unroll
-  for (int b = 0; b < 2; ++b)
+  for (int b = 0; b < BW; ++b)
 #pragma unroll
     for (int c = 0; c < NC; ++c) acc[b][c] = float4_t{0.f, 0.f, 0.f, 0.f};
 
@@ -228,8 +240,8 @@ __global__ __launch_bounds__(64 * BG_WAVES) void bgemm_kernel(LinArgs g) {
           // the pair 2kl, 2kl + 1 of the step; past an odd last tile the second tile's
           // words decode to finite values that meet zero activations (xfold_kernel)
           if (st * KT + 2 * kl < ntl) {
-            const uint32_t* p0 = mystg;                 // band 2bp: tiles 2kl, 2kl + 1
-            const uint32_t* p1 = mystg + TPL * NWK;     // band 2bp + 1
+            const uint32_t* p0 = mystg;                 // band 2bg: tiles 2kl, 2kl + 1
+            const uint32_t* p1 = mystg + TPL * NWK;     // band 2bg + 1
             const half8_t A0 = decode_a_pair<K, CB, V>(p0[qp.wa], p0[qp.wb], p0[NWK + qp.wa],
                                                        p0[NWK + qp.wb], qp.sh);
             const half8_t A1 = decode_a_pair<K, CB, V>(p1[qp.wa], p1[qp.wb], p1[NWK + qp.wa],
@@ -245,14 +257,18 @@ __global__ __launch_bounds__(64 * BG_WAVES) void bgemm_kernel(LinArgs g) {
         } else {
 #pragma unroll
           for (int t = 0; t < TPL; ++t) {
-            const int j = kl + BG_KL * t;            // tile of the step
+            const int j = kl + KL * t;               // tile of the step
             if (st * KT + j < ntl) {
-              const uint32_t* t0 = mystg + t * NWK;
-              const uint32_t* t1 = mystg + (TPL + t) * NWK;
               // every LDS read of the tile (window words, the NC B fragments) before the
               // decode, so the fragments' latency hides behind it (read just before each
               // MFMA pair, it was exposed)
-              const uint32_t w0a = t0[qp.wa], w0b = t0[qp.wb], w1a = t1[qp.wa], w1b = t1[qp.wb];
+              uint32_t wa[BW], wb[BW];
+#pragma unroll
+              for (int b = 0; b < BW; ++b) {
+                const uint32_t* tb = mystg + (b * TPL + t) * NWK;   // band BW * bg + b
+                wa[b] = tb[qp.wa];
+                wb[b] = tb[qp.wb];
+              }
               half8_t Bf[NC];
 #pragma unroll
               for (int c = 0; c < NC; ++c)
@@ -261,12 +277,12 @@ __global__ __launch_bounds__(64 * BG_WAVES) void bgemm_kernel(LinArgs g) {
               // fragment's read back in front of its MFMAs); with 8 chunks the fragments'
               // registers would spill
               if constexpr (NC <= 4) __builtin_amdgcn_sched_barrier(0);
-              const half8_t A0 = decode_a<K, CB, V>(w0a, w0b, qp.sh);
-              const half8_t A1 = decode_a<K, CB, V>(w1a, w1b, qp.sh);
 #pragma unroll
-              for (int c = 0; c < NC; ++c) {
-                acc[0][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, Bf[c], acc[0][c], 0, 0, 0);
-                acc[1][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, Bf[c], acc[1][c], 0, 0, 0);
+              for (int b = 0; b < BW; ++b) {
+                const half8_t A = decode_a<K, CB, V>(wa[b], wb[b], qp.sh);
+#pragma unroll
+                for (int c = 0; c < NC; ++c)
+                  acc[b][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bf[c], acc[b][c], 0, 0, 0);
               }
             }
           }
@@ -281,14 +297,14 @@ __global__ __launch_bounds__(64 * BG_WAVES) void bgemm_kernel(LinArgs g) {
 
   // ---- t[batch col][row] in LDS, k-lanes added in a fixed order: lane (n, gq) of band
   // b, chunk c holds rows 4gq .. 4gq + 3 (one float4)
-  for (int k2 = 0; k2 < BG_KL; k2 += NR) {
+  for (int k2 = 0; k2 < KL; k2 += NR) {
     if (kl >= k2 && kl < k2 + NR) {
       float* reg = tl + (kl - k2) * NR_OFF;
 #pragma unroll
-      for (int b = 0; b < 2; ++b)
+      for (int b = 0; b < BW; ++b)
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
-          float4_t* p = reinterpret_cast<float4_t*>(&reg[(c * 16 + r) * TLS + 32 * bp + 16 * b + 4 * gq]);
+          float4_t* p = reinterpret_cast<float4_t*>(&reg[(c * 16 + r) * TLS + 16 * (BW * bg + b) + 4 * gq]);
           *p = k2 == 0 ? acc[b][c] : *p + acc[b][c];
         }
     }
