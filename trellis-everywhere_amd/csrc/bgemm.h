@@ -3,7 +3,7 @@
 //
 // A workgroup of 16 waves owns one 128-row output block (the out-dim Hadamard block) x
 // NB = 16*NC batch columns x one k-range of `kr` tile columns, walked in steps of KT tiles
-// (16 at 16 columns, 8, or 4 at 128 columns). Wave w = (band group bg = w % NG, k-lane
+// (16 at 16 columns, 8, or 4 at 128 columns: the fp16-weight mode above 64). Wave w = (band group bg = w % NG, k-lane
 // kl = w / NG), a band group being BW = 2 or 4 adjacent bands (NG = 8 / BW groups, KL =
 // 16 / NG k-lanes): the waves of a SIMD share a band group and split every step's tiles
 // between them (tile j of a step belongs to k-lane j % KL), so a SIMD always has four

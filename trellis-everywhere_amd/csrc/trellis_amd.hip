@@ -152,8 +152,9 @@ int gemv_kr(const trellis_desc* const* W, int count, int batch) {
   return best;
 }
 
-// Batch >= 2 (bgemm_kernel): NC 16-column batch chunks per workgroup (up to 128 columns),
-// a work item is one 128-row block x one column block x one k-range of kr tile columns
+// Batch >= 2 (bgemm_kernel): NC 16-column batch chunks per workgroup (up to 64 columns in
+// the exact mode, 128 in the fp16-weight mode), a work item is one 128-row block x one
+// column block x one k-range of kr tile columns
 // (a multiple of the k-step: 16 tiles at 16 columns, 8 up to 64 and in the fp16-weight
 // mode, else 4), run by one 16-wave workgroup per CU. kr minimises ceil(items/CUs) x the per-SIMD work
 // of an item (2 bands x kr tiles x (decode ~61 + NC MFMAs x ~19 cycles; fp16-weight mode
@@ -161,10 +162,14 @@ int gemv_kr(const trellis_desc* const* W, int count, int batch) {
 // launch (~1.5 us) and the partial blocks it moves (S x rows x NB x 4 bytes written and
 // read at ~2.5 KB per cycle), plus a start-up latency per round after the first.
 // TRELLIS_BGEMM_KR forces a value, TRELLIS_BGEMM_NC the column-block width.
-int bgemm_nc(int batch) {
+// Above 64 columns the exact mode keeps 64-column blocks (each tile decoded once per
+// block): its 128-column kernel holds 8 fragments and 16 accumulators at a 4-tile k-step
+// and spills (20 bytes per lane at K=3, 68 at K=2 and 4), and measured 12-25 % slower on
+// the 8B gate/up/down at batch 96 to 512 at K=3 (2.5x at K=2 and 4).
+int bgemm_nc(int batch, bool f16) {
   const int forced = env_int("TRELLIS_BGEMM_NC", 0);
   if (forced == 1 || forced == 2 || forced == 4 || forced == 8) return forced;
-  return batch <= 16 ? 1 : batch <= 32 ? 2 : batch <= 64 ? 4 : 8;
+  return batch <= 16 ? 1 : batch <= 32 ? 2 : batch <= 64 || !f16 ? 4 : 8;
 }
 
 int bgemm_kr(const trellis_desc* const* W, int count, int batch, int nc, bool f16) {
@@ -227,7 +232,7 @@ GroupPlan group_plan(const trellis_desc* const* W, int count, int batch, bool f1
   GroupPlan p;
   p.gemv = use_gemv(W, count, batch);
   p.nb = batch;
-  p.nc = bgemm_nc(batch);
+  p.nc = bgemm_nc(batch, f16);
   p.ncb = p.gemv ? 1 : (batch + 16 * p.nc - 1) / (16 * p.nc);
   p.kr = p.gemv ? gemv_kr(W, count, batch) : bgemm_kr(W, count, batch, p.nc, f16);
   p.kc = p.kr >= 32 ? 16 : 8;
