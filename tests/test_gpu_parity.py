@@ -222,6 +222,29 @@ def test_prefill_vs_oracle(te, gpu_device, n, k, batch):
         assert tn.rel_err(y[b], want[b]) < TOL
 
 
+@pytest.mark.parametrize("K", [2, 3, 4])
+def test_prefill_column_block_width(te, gpu_device, monkeypatch, K):
+    """Above 64 columns the exact mode runs 64-column blocks (its 128-column kernel would
+    spill registers and is not built); a forced width of 8 chunks is clamped to 4 there and
+    honoured in the fp16-weight mode. Every width gives the oracle's result, and the exact
+    mode's results are bit-identical between the planner's choice and the forced one."""
+    _say(f"[prefill width] K={K} batch=200")
+    bits, rec = tn.synthetic_record(512, 1024, K, seed=200 + K)
+    lin = make_linear(te, bits, rec, gpu_device)
+    x = np.random.default_rng(K).standard_normal((200, 1024)).astype(np.float16)
+    xt = torch.from_numpy(x).to(gpu_device)
+    want = tn.packed_linear_ref(bits, rec, x)
+    planned = lin(xt).cpu().numpy()
+    assert tn.rel_err(planned, want) < TOL
+    monkeypatch.setenv("TRELLIS_BGEMM_NC", "8")
+    forced = lin(xt).cpu().numpy()
+    assert np.array_equal(forced, planned)
+    f16 = lin(xt, mma_f16=True).cpu().numpy()
+    assert tn.rel_err(f16, want) < TOL
+    monkeypatch.setenv("TRELLIS_BGEMM_NC", "4")
+    assert tn.rel_err(lin(xt, mma_f16=True).cpu().numpy(), want) < TOL
+
+
 @pytest.mark.parametrize("batch", [16, 64])
 def test_batched_repeat_deterministic(te, gpu_device, batch):
     """Batched split-K: tickets reset themselves and repeated calls are bit-identical."""

@@ -109,6 +109,7 @@ template <int NC, int F16> struct BgBands {
 
 template <int K, int CB, int V, int NC, int F16>
 __global__ __launch_bounds__(64 * BG_WAVES) void bgemm_kernel(LinArgs g) {
+  static_assert(F16 || NC <= 4, "the exact mode runs at most 64 columns per workgroup");
   constexpr int NWK = 8 * K;
   constexpr int KT = BgStep<NC, F16>::KT;          // tile columns per k-step
   constexpr int BW = BgBands<NC, F16>::BW;         // bands per wave

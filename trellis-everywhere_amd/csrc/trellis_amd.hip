@@ -168,7 +168,8 @@ int gemv_kr(const trellis_desc* const* W, int count, int batch) {
 // the 8B gate/up/down at batch 96 to 512 at K=3 (2.5x at K=2 and 4).
 int bgemm_nc(int batch, bool f16) {
   const int forced = env_int("TRELLIS_BGEMM_NC", 0);
-  if (forced == 1 || forced == 2 || forced == 4 || forced == 8) return forced;
+  if (forced == 8) return f16 ? 8 : 4;
+  if (forced == 1 || forced == 2 || forced == 4) return forced;
   return batch <= 16 ? 1 : batch <= 32 ? 2 : batch <= 64 || !f16 ? 4 : 8;
 }
 
