@@ -224,10 +224,11 @@ def test_prefill_vs_oracle(te, gpu_device, n, k, batch):
 
 @pytest.mark.parametrize("K", [2, 3, 4])
 def test_prefill_column_block_width(te, gpu_device, monkeypatch, K):
-    """Above 64 columns the exact mode runs 64-column blocks (its 128-column kernel would
-    spill registers and is not built); a forced width of 8 chunks is clamped to 4 there and
-    honoured in the fp16-weight mode. Every width gives the oracle's result, and the exact
-    mode's results are bit-identical between the planner's choice and the forced one."""
+    """Above 64 columns the batched kernel runs 64-column blocks (16 waves) or, as the
+    planner's cost model decides, 128-column blocks (8 waves in the exact mode, whose
+    fragments and accumulators need two waves' worth of registers). Every width, forced
+    with TRELLIS_BGEMM_NC in either mode, gives the oracle's result, and the exact mode's
+    widths agree to fp32 summation order."""
     _say(f"[prefill width] K={K} batch=200")
     bits, rec = tn.synthetic_record(512, 1024, K, seed=200 + K)
     lin = make_linear(te, bits, rec, gpu_device)
@@ -236,13 +237,13 @@ def test_prefill_column_block_width(te, gpu_device, monkeypatch, K):
     want = tn.packed_linear_ref(bits, rec, x)
     planned = lin(xt).cpu().numpy()
     assert tn.rel_err(planned, want) < TOL
-    monkeypatch.setenv("TRELLIS_BGEMM_NC", "8")
-    forced = lin(xt).cpu().numpy()
-    assert np.array_equal(forced, planned)
-    f16 = lin(xt, mma_f16=True).cpu().numpy()
-    assert tn.rel_err(f16, want) < TOL
-    monkeypatch.setenv("TRELLIS_BGEMM_NC", "4")
-    assert tn.rel_err(lin(xt, mma_f16=True).cpu().numpy(), want) < TOL
+    for nc in ("8", "4"):
+        monkeypatch.setenv("TRELLIS_BGEMM_NC", nc)
+        forced = lin(xt).cpu().numpy()
+        assert tn.rel_err(forced, want) < TOL, nc
+        assert tn.rel_err(forced, planned) < 1e-5, nc
+        assert np.array_equal(forced, lin(xt).cpu().numpy()), nc      # deterministic
+        assert tn.rel_err(lin(xt, mma_f16=True).cpu().numpy(), want) < TOL, nc
 
 
 @pytest.mark.parametrize("batch", [16, 64])

@@ -1,15 +1,15 @@
 // bgemm.h — batched packed linear for gfx950 (batch 2 .. prefill): decode once, reuse
 // across the batch.
 //
-// A workgroup of 16 waves owns one 128-row output block (the out-dim Hadamard block) x
-// NB = 16*NC batch columns x one k-range of `kr` tile columns, walked in steps of KT tiles
-// (16 at 16 columns, 8, or 4 at 128 columns: the fp16-weight mode above 64). Wave w = (band group bg = w % NG, k-lane
-// kl = w / NG), a band group being BW = 2 or 4 adjacent bands (NG = 8 / BW groups, KL =
-// 16 / NG k-lanes): the waves of a SIMD share a band group and split every step's tiles
-// between them (tile j of a step belongs to k-lane j % KL), so a SIMD always has four
-// waves to switch between:
+// A workgroup of 16 waves (8 for the exact mode's 128-column blocks) owns one 128-row
+// output block (the out-dim Hadamard block) x NB = 16*NC batch columns x one k-range of
+// `kr` tile columns, walked in steps of KT tiles (16 at 16 columns, 8, or 4 at 128
+// columns). Wave w = (band group bg = w % NG, k-lane kl = w / NG), a band group being
+// BW = 2 or 4 adjacent bands (NG = 8 / BW groups, KL = waves / NG k-lanes): the waves of a
+// SIMD share a band group and split every step's tiles between them (tile j of a step
+// belongs to k-lane j % KL), so a SIMD has four (or two) waves to switch between:
 //   * the B tile of a step (xf[batch cols][KT*16] as (x, x) fp16 pairs written by
-//     xfold_kernel) is loaded two steps ahead into registers by all 1024 threads, stored
+//     xfold_kernel) is loaded two steps ahead into registers by all the threads, stored
 //     to one half of a double-buffered LDS area, and read by every wave: each fragment
 //     serves the BW bands of each of the NG band groups; one barrier per step;
 //   * each wave's packed words ride a two-step register ring and a wave-private LDS
@@ -97,7 +97,12 @@ __device__ __forceinline__ void bg_out_fold(const LinArgs& g, const LinMat& m, c
 template <int NC, int F16> struct BgStep {
   static constexpr int KT = F16 ? 8 : NC == 1 ? 16 : NC <= 4 ? 8 : 4;
 };
-constexpr int BG_WAVES = 16;
+// waves per workgroup: 16 (four per SIMD), or 8 (two per SIMD, 256 registers each) for the
+// exact mode's 128-column blocks, whose 8 fragments and 16 accumulators per wave do not fit
+// a quarter of a SIMD's registers
+template <int NC, int F16> struct BgWaves {
+  static constexpr int WV = (!F16 && NC == 8) ? 8 : 16;
+};
 // bands per wave: 4 at 16 batch columns (8 k-lanes: each B fragment read from LDS feeds 4
 // bands instead of 2; the 8B gate+up group at batch 16 27.8 -> 26.6-27.1 us), otherwise 2
 // (a band pair, 4 k-lanes: at 32 and 64 columns 4 bands measured no faster on gate+up and
@@ -108,8 +113,8 @@ template <int NC, int F16> struct BgBands {
 };
 
 template <int K, int CB, int V, int NC, int F16>
-__global__ __launch_bounds__(64 * BG_WAVES) void bgemm_kernel(LinArgs g) {
-  static_assert(F16 || NC <= 4, "the exact mode runs at most 64 columns per workgroup");
+__global__ __launch_bounds__((64 * BgWaves<NC, F16>::WV)) void bgemm_kernel(LinArgs g) {
+  constexpr int BG_WAVES = BgWaves<NC, F16>::WV;
   constexpr int NWK = 8 * K;
   constexpr int KT = BgStep<NC, F16>::KT;          // tile columns per k-step
   constexpr int BW = BgBands<NC, F16>::BW;         // bands per wave

@@ -92,17 +92,10 @@ template <int K, int CB, int V, int F16>
 static int launch_bgemm_nc(int nc, const LinArgs& g, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(g.total));
   switch (nc) {
-    case 1: hipLaunchKernelGGL((bgemm_kernel<K, CB, V, 1, F16>), grid, dim3(64 * BG_WAVES), 0, st, g); break;
-    case 2: hipLaunchKernelGGL((bgemm_kernel<K, CB, V, 2, F16>), grid, dim3(64 * BG_WAVES), 0, st, g); break;
-    case 4: hipLaunchKernelGGL((bgemm_kernel<K, CB, V, 4, F16>), grid, dim3(64 * BG_WAVES), 0, st, g); break;
-    default:
-      // 128 columns: the fp16-weight mode only (the planner keeps the exact mode at 64
-      // columns, where its 128-column form would spill registers)
-      if constexpr (F16)
-        hipLaunchKernelGGL((bgemm_kernel<K, CB, V, 8, F16>), grid, dim3(64 * BG_WAVES), 0, st, g);
-      else
-        return 13;
-      break;
+    case 1: hipLaunchKernelGGL((bgemm_kernel<K, CB, V, 1, F16>), grid, dim3(64 * BgWaves<1, F16>::WV), 0, st, g); break;
+    case 2: hipLaunchKernelGGL((bgemm_kernel<K, CB, V, 2, F16>), grid, dim3(64 * BgWaves<2, F16>::WV), 0, st, g); break;
+    case 4: hipLaunchKernelGGL((bgemm_kernel<K, CB, V, 4, F16>), grid, dim3(64 * BgWaves<4, F16>::WV), 0, st, g); break;
+    default: hipLaunchKernelGGL((bgemm_kernel<K, CB, V, 8, F16>), grid, dim3(64 * BgWaves<8, F16>::WV), 0, st, g); break;
   }
   return hipGetLastError() == hipSuccess ? 0 : 13;
 }

@@ -152,42 +152,32 @@ int gemv_kr(const trellis_desc* const* W, int count, int batch) {
   return best;
 }
 
-// Batch >= 2 (bgemm_kernel): NC 16-column batch chunks per workgroup (up to 64 columns in
-// the exact mode, 128 in the fp16-weight mode), a work item is one 128-row block x one
-// column block x one k-range of kr tile columns
+// Batch >= 2 (bgemm_kernel): NC 16-column batch chunks per workgroup (up to 128 columns),
+// a work item is one 128-row block x one column block x one k-range of kr tile columns
 // (a multiple of the k-step: 16 tiles at 16 columns, 8 up to 64 and in the fp16-weight
-// mode, else 4), run by one 16-wave workgroup per CU. kr minimises ceil(items/CUs) x the per-SIMD work
-// of an item (2 bands x kr tiles x (decode ~61 + NC MFMAs x ~19 cycles; fp16-weight mode
-// ~75 + NC x ~10)) plus, with split-K, the bfold_kernel
-// launch (~1.5 us) and the partial blocks it moves (S x rows x NB x 4 bytes written and
-// read at ~2.5 KB per cycle), plus a start-up latency per round after the first.
-// TRELLIS_BGEMM_KR forces a value, TRELLIS_BGEMM_NC the column-block width.
-// Above 64 columns the exact mode keeps 64-column blocks (each tile decoded once per
-// block): its 128-column kernel holds 8 fragments and 16 accumulators at a 4-tile k-step
-// and spills (20 bytes per lane at K=3, 68 at K=2 and 4), and measured 12-25 % slower on
-// the 8B gate/up/down at batch 96 to 512 at K=3 (2.5x at K=2 and 4).
-int bgemm_nc(int batch, bool f16) {
-  const int forced = env_int("TRELLIS_BGEMM_NC", 0);
-  if (forced == 8) return f16 ? 8 : 4;
-  if (forced == 1 || forced == 2 || forced == 4) return forced;
-  return batch <= 16 ? 1 : batch <= 32 ? 2 : batch <= 64 || !f16 ? 4 : 8;
-}
-
-int bgemm_kr(const trellis_desc* const* W, int count, int batch, int nc, bool f16) {
+// mode, else 4), run by one workgroup per CU (16 waves; 8 for the exact mode's 128-column
+// blocks). kr minimises ceil(items/CUs) x the per-SIMD work of an item (2 bands x kr tiles
+// x (decode ~61 + NC MFMAs x ~19 cycles; fp16-weight mode ~75 + NC x ~10; ~258 for the
+// exact mode's 128-column blocks, whose two waves per SIMD hide less)) plus, with split-K,
+// the bfold_kernel launch (~1.5 us) and the partial blocks it moves (S x rows x NB x 4
+// bytes written and read at ~2.5 KB per cycle), plus a start-up latency per round after
+// the first. TRELLIS_BGEMM_KR forces a value, TRELLIS_BGEMM_NC the column-block width.
+static int bgemm_kr_cost(const trellis_desc* const* W, int count, int batch, int nc, bool f16,
+                         long long* cost) {
   int maxt = 0;
   for (int i = 0; i < count; ++i) maxt = W[i]->k_in / 16 > maxt ? W[i]->k_in / 16 : maxt;
   const int kt = f16 ? 8 : nc == 1 ? 16 : nc <= 4 ? 8 : 4;   // BgStep<nc, f16>::KT
   // per band-tile SIMD cycles: the decode and NC MFMAs (the fp16-weight mode decodes a
   // little more and issues half the MFMAs)
-  const long long tile_cost = f16 ? 75 + 10 * nc : 61 + 19 * nc;
+  const long long tile_cost = f16 ? 75 + 10 * nc : nc == 8 ? 258 : 61 + 19 * nc;
   const int cap = ((maxt + kt - 1) / kt) * kt;
-  const int forced = env_int("TRELLIS_BGEMM_KR", 0);
-  if (forced >= kt && forced % kt == 0) return forced < cap ? forced : cap;
   const long long cus = device_cus();
   const long long ncb = (batch + 16 * nc - 1) / (16 * nc);
+  const int forced = env_int("TRELLIS_BGEMM_KR", 0);
+  const bool force = forced >= kt && forced % kt == 0;
   int best = cap;
   long long best_cost = -1;
-  for (int kr = kt; kr <= cap; kr += kt) {
+  for (int kr = force ? (forced < cap ? forced : cap) : kt; kr <= cap; kr += kt) {
     long long items = 0, part_bytes = 0;
     int smax = 1;
     for (int i = 0; i < count; ++i) {
@@ -197,16 +187,42 @@ int bgemm_kr(const trellis_desc* const* W, int count, int batch, int nc, bool f1
       smax = S > smax ? S : smax;
       if (S > 1) part_bytes += static_cast<long long>(S) * n_ob * ncb * 128 * 16 * nc * 4;
     }
-    if (smax > 16) continue;
+    if (smax > 16 && !force) continue;
     const long long rounds = (items + cus - 1) / cus;
     const long long epi = smax > 1 ? 3600 + 2 * part_bytes / 2500 : 0;
-    const long long cost = rounds * kr * 2 * tile_cost + epi + (rounds - 1) * 3600;
-    if (best_cost < 0 || cost < best_cost) {
+    const long long c = rounds * kr * 2 * tile_cost + epi + (rounds - 1) * 3600;
+    if (best_cost < 0 || c < best_cost) {
       best = kr;
-      best_cost = cost;
+      best_cost = c;
     }
+    if (force) break;
   }
+  *cost = best_cost;
   return best;
+}
+
+int bgemm_kr(const trellis_desc* const* W, int count, int batch, int nc, bool f16) {
+  long long cost;
+  return bgemm_kr_cost(W, count, batch, nc, f16, &cost);
+}
+
+// Column-block width: 16, 32 or 64 columns up to batch 64; above, the fp16-weight mode
+// takes 128, and the exact mode 64 (four waves per SIMD) or 128 (two waves per SIMD, each
+// tile decoded half as often), whichever the cost model above finds cheaper for the group
+// (8B block at batch 512: q/k/v and gate+up at 128 columns, 100 -> 87 and 277 -> 243 us;
+// o stays at 64, where 128 measured 53 -> 57 us; one gate projection at batch 96 stays at 64,
+// at 256 takes 128: 92 -> 76 us).
+int bgemm_nc(const trellis_desc* const* W, int count, int batch, bool f16) {
+  const int forced = env_int("TRELLIS_BGEMM_NC", 0);
+  if (forced == 1 || forced == 2 || forced == 4 || forced == 8) return forced;
+  if (batch <= 16) return 1;
+  if (batch <= 32) return 2;
+  if (batch <= 64) return 4;
+  if (f16) return 8;
+  long long c4, c8;
+  bgemm_kr_cost(W, count, batch, 4, false, &c4);
+  bgemm_kr_cost(W, count, batch, 8, false, &c8);
+  return c8 < c4 ? 8 : 4;
 }
 
 // The decode-GEMV for batch 1 to 4, and for 5 to 16 when its items at the longest k-range
@@ -233,7 +249,7 @@ GroupPlan group_plan(const trellis_desc* const* W, int count, int batch, bool f1
   GroupPlan p;
   p.gemv = use_gemv(W, count, batch);
   p.nb = batch;
-  p.nc = bgemm_nc(batch, f16);
+  p.nc = bgemm_nc(W, count, batch, f16);
   p.ncb = p.gemv ? 1 : (batch + 16 * p.nc - 1) / (16 * p.nc);
   p.kr = p.gemv ? gemv_kr(W, count, batch) : bgemm_kr(W, count, batch, p.nc, f16);
   p.kc = p.kr >= 32 ? 16 : 8;
