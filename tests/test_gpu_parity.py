@@ -222,15 +222,16 @@ def test_prefill_vs_oracle(te, gpu_device, n, k, batch):
         assert tn.rel_err(y[b], want[b]) < TOL
 
 
-@pytest.mark.parametrize("K", [2, 3, 4])
-def test_prefill_column_block_width(te, gpu_device, monkeypatch, K):
+@pytest.mark.parametrize("K,cb,V", [(2, "mcg", 1), (3, "mcg", 1), (4, "mcg", 1), (3, "3inst", 2),
+                                    (3, "1mad", 1), (4, "3inst", 1), (2, "1mad", 2)])
+def test_prefill_column_block_width(te, gpu_device, monkeypatch, K, cb, V):
     """Above 64 columns the batched kernel runs 64-column blocks (16 waves) or, as the
     planner's cost model decides, 128-column blocks (8 waves in the exact mode, whose
     fragments and accumulators need two waves' worth of registers). Every width, forced
     with TRELLIS_BGEMM_NC in either mode, gives the oracle's result, and the exact mode's
     widths agree to fp32 summation order."""
-    _say(f"[prefill width] K={K} batch=200")
-    bits, rec = tn.synthetic_record(512, 1024, K, seed=200 + K)
+    _say(f"[prefill width] K={K} cb={cb} V={V} batch=200")
+    bits, rec = tn.synthetic_record(512, 1024, K, seed=200 + K, codebook=cb, V=V)
     lin = make_linear(te, bits, rec, gpu_device)
     x = np.random.default_rng(K).standard_normal((200, 1024)).astype(np.float16)
     xt = torch.from_numpy(x).to(gpu_device)
