@@ -109,8 +109,9 @@ int trellis_workspace_bytes(const trellis_desc *W, int batch, size_t *bytes);
  * Batch 1 to 4 runs one decode-GEMV launch (gemv_kernel, x fold fused; the batch rows
  * ride the MFMA's columns), and so does batch 5 to 16 when that launch's work items fit one
  * round on the CUs. Other calls run the x fold once (xfold_kernel), then the
- * decode-once batched kernel (bgemm_kernel: each weight tile decoded once per 128 batch
- * columns and fed to exact fp16 MFMAs), and, when the launch plan splits k, the slice
+ * decode-once batched kernel (bgemm_kernel: each weight tile decoded once per 16 to 128
+ * batch columns, as the launch plan chooses, and fed to exact fp16 MFMAs), and, when the
+ * launch plan splits k, the slice
  * reduction and output fold (bfold_kernel). */
 int trellis_packed_linear(const trellis_desc *W, const void *x, int64_t ldx, int batch,
                           int x_dtype, void *y, int64_t ldy, int y_dtype, void *workspace,
