@@ -3,7 +3,8 @@ inputs copied in and eager calls of the same linears between the replays, must e
 eager call on the same inputs bit for bit. Covers the batch-1 split-K tickets (reset by the
 kernels, no memset in the graph), the decode-GEMV with 4 and 16 rows in its MFMA columns
 (batch 3, 12; split k, one ticket per workgroup), the batched path with its x-fold and
-split-K fold launches, and the fp16-weight mode."""
+split-K fold launches (at 64 and 200 columns, the latter also forced to 128-column blocks),
+and the fp16-weight mode."""
 import sys
 
 import numpy as np
@@ -26,10 +27,15 @@ def make_linear(te, bits, rec, device):
     return te.PackedLinear(r, device=device)
 
 
-@pytest.mark.parametrize("batch,mma_f16", [(1, False), (3, False), (12, False), (64, False),
-                                           (64, True)])
-def test_graph_replays_match_eager(te, gpu_device, batch, mma_f16):
-    _say(f"[graph] batch={batch} mma_f16={mma_f16}")
+@pytest.mark.parametrize("batch,mma_f16,nc", [(1, False, None), (3, False, None), (12, False, None),
+                                              (64, False, None), (64, True, None),
+                                              (200, False, None), (200, False, "8")])
+def test_graph_replays_match_eager(te, gpu_device, monkeypatch, batch, mma_f16, nc):
+    """nc forces the batched kernel's column-block width (8 chunks: the exact mode's
+    two-wave 128-column kernel)."""
+    _say(f"[graph] batch={batch} mma_f16={mma_f16} nc={nc}")
+    if nc is not None:
+        monkeypatch.setenv("TRELLIS_BGEMM_NC", nc)
     shapes = [(1024, 2048), (256, 2048), (512, 2048)]      # split-K plans at every batch
     lins = []
     for i, (n, k) in enumerate(shapes):

@@ -62,9 +62,9 @@ def _check(te, cases, grp, batch, rng, device):
 
 def test_noalloc_matches_group_ex(te, gpu_device):
     rng = np.random.default_rng(2024)
-    # split-K at batch 1 (tickets in the scratch header), the batched path at 64
+    # split-K at batch 1 (tickets in the scratch header), the batched path at 200 and 64
     cases, grp = _group(te, [(1024, 2048), (256, 2048), (384, 2048)], 500, gpu_device)
-    for batch in (64, 3, 1):
+    for batch in (200, 64, 3, 1):
         _say(f"[noalloc] group A batch={batch}")
         _check(te, cases, grp, batch, rng, gpu_device)
     # another group's call after group A's batch-64 data filled the scratch: its ticket
