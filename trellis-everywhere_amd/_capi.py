@@ -30,6 +30,7 @@ NOALLOC_SCRATCH_BYTES = 32 << 20
 
 # enum trellis_flags
 MMA_F16 = 1
+ERR_WORKSPACE = 10   # TRELLIS_ERR_WORKSPACE: returned before anything is launched
 
 # every symbol include/trellis_amd.h declares
 EXPORTED = ("trellis_workspace_bytes", "trellis_packed_linear", "trellis_decode_tiles",

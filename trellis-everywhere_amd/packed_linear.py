@@ -140,13 +140,24 @@ class PackedLinear:
         if B == 0:
             # no rows, nothing to launch (the C ABI rejects a batch of 0)
             return out
-        ws = workspace if workspace is not None else self._workspace(B)
-        stream = torch.cuda.current_stream(self.device).cuda_stream
-        st = lib.trellis_packed_linear_ex(
-            ctypes.byref(self.desc), _ptr(x2), x2.stride(0), B,
-            _capi.DT_F16 if x2.dtype == torch.float16 else _capi.DT_F32,
-            _ptr(y2), y2.stride(0), _capi.DT_F16 if y2.dtype == torch.float16 else _capi.DT_F32,
-            _ptr(ws), ws.numel(), _capi.MMA_F16 if mma_f16 else 0, ctypes.c_void_p(stream))
+        stream = ctypes.c_void_p(torch.cuda.current_stream(self.device).cuda_stream)
+        xdt = _capi.DT_F16 if x2.dtype == torch.float16 else _capi.DT_F32
+        ydt = _capi.DT_F16 if y2.dtype == torch.float16 else _capi.DT_F32
+        flags = _capi.MMA_F16 if mma_f16 else 0
+
+        def launch(ws):
+            return lib.trellis_packed_linear_ex(
+                ctypes.byref(self.desc), _ptr(x2), x2.stride(0), B, xdt, _ptr(y2), y2.stride(0),
+                ydt, _ptr(ws), ws.numel(), flags, stream)
+
+        if workspace is not None:
+            st = launch(workspace)
+        else:
+            # the library checks the workspace size before it launches anything, so the
+            # current buffer is tried first and sized (grown) only when it is too small
+            st = launch(self._ws) if self._ws is not None else _capi.ERR_WORKSPACE
+            if st == _capi.ERR_WORKSPACE:
+                st = launch(self._workspace(B))
         _capi.check(st)
         return out[0] if (squeeze and out.dim() == 2) else out
 
@@ -253,16 +264,23 @@ class PackedGroup:
         if B == 0:
             # no rows: every member's output is [0, n_i], nothing to launch
             return outs
-        ws = self._workspace(B)
         xp = (ctypes.c_void_p * n)(*[x.data_ptr() for x in x2])
         yp = (ctypes.c_void_p * n)(*[y.data_ptr() for y in y2])
         ldx = (ctypes.c_int64 * n)(*[x.stride(0) for x in x2])
         ldy = (ctypes.c_int64 * n)(*[y.stride(0) for y in y2])
-        stream = torch.cuda.current_stream(self.device).cuda_stream
-        _capi.check(lib.trellis_packed_linear_group_ex(
-            self._dptrs, n, xp, ldx, B, _capi.DT_F16 if dt == torch.float16 else _capi.DT_F32,
-            yp, ldy, _capi.DT_F16 if ydt == torch.float16 else _capi.DT_F32,
-            _ptr(ws), ws.numel(), _capi.MMA_F16 if mma_f16 else 0, ctypes.c_void_p(stream)))
+        stream = ctypes.c_void_p(torch.cuda.current_stream(self.device).cuda_stream)
+
+        def launch(ws):
+            return lib.trellis_packed_linear_group_ex(
+                self._dptrs, n, xp, ldx, B, _capi.DT_F16 if dt == torch.float16 else _capi.DT_F32,
+                yp, ldy, _capi.DT_F16 if ydt == torch.float16 else _capi.DT_F32,
+                _ptr(ws), ws.numel(), _capi.MMA_F16 if mma_f16 else 0, stream)
+
+        # as PackedLinear.forward: the current workspace first, sized only when too small
+        st = launch(self._ws) if self._ws is not None else _capi.ERR_WORKSPACE
+        if st == _capi.ERR_WORKSPACE:
+            st = launch(self._workspace(B))
+        _capi.check(st)
         if squeeze:
             return [o[0] if o.dim() == 2 else o for o in outs]
         return outs
