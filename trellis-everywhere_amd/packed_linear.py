@@ -20,6 +20,17 @@ def _ptr(t: torch.Tensor) -> int:
     return t.data_ptr()
 
 
+# the current stream's handle on a device: torch's raw accessor (0.1 us) where it exists,
+# else the public one (~2 us per call, a fifth of an eager call's host cost)
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _stream(device: torch.device) -> int:
+    if _raw_stream is not None and device.index is not None:
+        return _raw_stream(device.index)
+    return torch.cuda.current_stream(device).cuda_stream
+
+
 def _grow_workspace(owner, need: int) -> torch.Tensor:
     """The owner's workspace, replaced by a larger zero-filled one when `need` exceeds it
     (every call leaves its counters at zero again, so a workspace is zero-filled once).
@@ -140,7 +151,7 @@ class PackedLinear:
         if B == 0:
             # no rows, nothing to launch (the C ABI rejects a batch of 0)
             return out
-        stream = ctypes.c_void_p(torch.cuda.current_stream(self.device).cuda_stream)
+        stream = ctypes.c_void_p(_stream(self.device))
         xdt = _capi.DT_F16 if x2.dtype == torch.float16 else _capi.DT_F32
         ydt = _capi.DT_F16 if y2.dtype == torch.float16 else _capi.DT_F32
         flags = _capi.MMA_F16 if mma_f16 else 0
@@ -169,7 +180,7 @@ class PackedLinear:
         total = (self.n_out // 16) * (self.k_in // 16)
         nt = total - tile_begin if ntiles is None else ntiles
         out = torch.empty((nt, 256), dtype=torch.float32, device=self.device)
-        stream = torch.cuda.current_stream(self.device).cuda_stream
+        stream = _stream(self.device)
         _capi.check(lib.trellis_decode_tiles(ctypes.byref(self.desc), tile_begin, nt, _ptr(out),
                                              ctypes.c_void_p(stream)))
         return out
@@ -191,7 +202,7 @@ class PackedLinear:
             raise ValueError(f"out must be [{nt}, {self.k_in}] with unit column stride")
         if out.dtype not in (torch.float16, torch.float32):
             raise ValueError(f"out dtype {out.dtype} not supported")
-        stream = torch.cuda.current_stream(self.device).cuda_stream
+        stream = _stream(self.device)
         _capi.check(lib.trellis_embed_rows(
             ctypes.byref(self.desc), _ptr(tok), nt, _ptr(out), out.stride(0),
             _capi.DT_F16 if out.dtype == torch.float16 else _capi.DT_F32,
@@ -268,7 +279,7 @@ class PackedGroup:
         yp = (ctypes.c_void_p * n)(*[y.data_ptr() for y in y2])
         ldx = (ctypes.c_int64 * n)(*[x.stride(0) for x in x2])
         ldy = (ctypes.c_int64 * n)(*[y.stride(0) for y in y2])
-        stream = ctypes.c_void_p(torch.cuda.current_stream(self.device).cuda_stream)
+        stream = ctypes.c_void_p(_stream(self.device))
 
         def launch(ws):
             return lib.trellis_packed_linear_group_ex(
@@ -319,7 +330,7 @@ def encode_tiles(w: torch.Tensor, K: int, codebook: str = "mcg", want_dq: bool =
     nbytes = ctypes.c_size_t(0)
     _capi.check(lib.trellis_encode_workspace_bytes(int(K), nt, ctypes.byref(nbytes)))
     ws = torch.empty(max(int(nbytes.value), 256), dtype=torch.uint8, device=w.device)
-    stream = torch.cuda.current_stream(w.device).cuda_stream
+    stream = _stream(w.device)
     _capi.check(lib.trellis_encode_tiles(_ptr(w), nt, int(K), _capi.CB_IDS[codebook], _ptr(bits),
                                          _ptr(dq) if want_dq else None, _ptr(ws), ws.numel(),
                                          ctypes.c_void_p(stream)))
