@@ -36,3 +36,14 @@ def test_dram_counters_agree_with_the_scaled_fetch():
 
 def test_traffic_absent_file_is_none(tmp_path):
     assert bench.traffic_from_profile(str(tmp_path / "missing.txt")) is None
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py --gpus N with N > 1 exits with a message (one GPU is what this build measures),
+    before it touches the GPU."""
+    import json
+    import subprocess
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in json.loads(r.stdout.strip().splitlines()[-1])["error"]
