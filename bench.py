@@ -11,8 +11,8 @@ HBM; to defeat the 256 MB Infinity Cache the steps rotate over `copies` distinct
 
 value = packed-weight bytes of the block / seconds per step (GB/s, algorithmic bytes
 n*k*K/8). The JSON line also carries us/layer, the dominant launch's HBM roofline (gate+up,
-duration from HIP events on the launch stream), the same block at batch 16 and 64 with
-their fp16 MFMA rooflines (algorithmic 2*B*n*k flops), and a CPU baseline: this repo's torch-CPU
+duration from HIP events on the launch stream), the same block at batch 16 and 64 and at a
+512-token prefill with their fp16 MFMA rooflines (algorithmic 2*B*n*k flops), and a CPU baseline: this repo's torch-CPU
 restatement of the reference decode+restore+matmul (oracle/torch_cpu.py) on a bounded
 sample, per configuration and layer. The bit-rate sweep (configs[4]: K=2,3,4 x V=1,2 on
 the 8B gate/up/down shapes, at batch 1 and at a 512-token prefill) runs by default
@@ -413,6 +413,7 @@ def batched_figure(te, torch, dev, bs, K, V, args, samples=None):
     fl = block_flops(LAYERS, bs)
     dom_fl = 2 * bs * 2 * 12288 * 4096
     dom_tf = dom_fl / (grp[DOMINANT] * 1e-6) / 1e12
+    # the planner's width for gate+up (above 64 columns: 128 here, by its cost model)
     nc = 1 if bs <= 16 else 2 if bs <= 32 else 4 if bs <= 64 else 8
     out = {"us_per_block": round(sec * 1e6, 2),
            "tflops": round(fl / sec / 1e12, 2),
@@ -492,7 +493,8 @@ def main():
     ap.add_argument("--batch", type=int, default=1, help="headline batch (default 1)")
     ap.add_argument("--K", type=int, default=3)
     ap.add_argument("--V", type=int, default=1)
-    ap.add_argument("--no-batch64", action="store_true", help="skip the batch-16 and batch-64 MFMA figures")
+    ap.add_argument("--no-batch64", action="store_true",
+                    help="skip the batch-16, batch-64 and 512-prefill MFMA figures")
     ap.add_argument("--weight-copies", type=int, default=None,
                     help="distinct weight copies the steps rotate over (default: >= 1 GB of "
                          "packed bits, beyond the 256 MB MALL; 1 keeps a block resident in it)")
@@ -538,7 +540,7 @@ def main():
 
     batched = {}
     if not args.no_batch64 and B == 1:
-        for bs in (16, 64):
+        for bs in (16, 64, 512):
             batched[bs] = batched_figure(te, torch, dev, bs, K, V, args, samples)
     batch64 = batched.get(64)
 
@@ -590,6 +592,7 @@ def main():
                    "us_per_layer_single_launch": us_layer,
                    "batch16": batched.get(16),
                    "batch64": batch64,
+                   "prefill512": batched.get(512),
                    "sweep_configs4": sweep,
                    "next_rows": extra},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
