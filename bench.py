@@ -342,10 +342,12 @@ def check_outputs(samples, tol=OUTPUT_TOL):
     return res
 
 
-def extras(te, torch, dev, steps, K=4):
+def extras(te, torch, dev, steps, K=4, samples=None):
     """Next-row measurements on a Qwen3-8B vocab matrix (151936 x 4096, K=4, as the 8B export
     quantizes the LM head): the batch-1 LM-head GEMV, and embedding-row lookups
-    (trellis_embed_rows) of 1 and 512 random token ids; 4 weight copies (1.2 GB) rotated."""
+    (trellis_embed_rows) of 1 and 512 random token ids; 4 weight copies (1.2 GB) rotated.
+    With a `samples` list, the LM head's output of its last timed launch (the last weight
+    copy) is sampled for the output check (take_samples)."""
     n, k = 151936, 4096
     copies = 4
     mats = [make_layers(te, torch, dev, [("lm_head", n, k)], K, 1, seed=100 + c)["lm_head"]
@@ -375,6 +377,10 @@ def extras(te, torch, dev, steps, K=4):
         return e0.elapsed_time(e1) * 1e3 / (reps * copies)
 
     us_head = timed(lambda c: mats[c].forward(x, out=y))
+    if samples is not None:
+        # every replay writes y from copy 0 to copy `copies - 1`, in that order
+        samples.extend(take_samples({"lm_head": mats[-1]}, {"lm_head": x[None]}, {"lm_head": y[None]},
+                                    [("lm_head", n, k)], "lm_head batch 1", 3))
     # the encoder row: trellis_encode_tiles on 4096 tiles (16 per workgroup), K=3 MCG
     wt = torch.randn((4096, 256), device=dev)
     te.encode_tiles(wt[:256], 3, "mcg", want_dq=False)
@@ -552,7 +558,7 @@ def main():
     extra = None
     if not args.no_extras and B == 1:
         log("[bench] extras: LM head (K=4) and embedding rows")
-        extra = extras(te, torch, dev, max(40, args.steps // 5))
+        extra = extras(te, torch, dev, max(40, args.steps // 5), samples=samples)
         # small decode batches (the decode-GEMV carries the rows in its MFMA columns)
         small = {}
         for bs in (2, 4, 8):

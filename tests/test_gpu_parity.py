@@ -175,6 +175,24 @@ def test_qwen3_8b_shapes_sampled_blocks(te, gpu_device, name, n, k):
     assert (lhs - rhs).abs().max().item() / rhs.abs().max().item() < TOL
 
 
+@pytest.mark.parametrize("batch", [1, 3])
+def test_lm_head_shape_sampled_blocks(te, gpu_device, batch):
+    """The Qwen3-8B vocab matrix at K=4 (151936 x 4096, the LM head the bench times): 1187
+    output blocks, so the decode-GEMV's work items run in several rounds over the CUs.
+    Blocks of the first, middle and last rounds against the oracle, every batch row."""
+    _say(f"[lm head] 151936x4096 K=4 batch={batch}")
+    n, k = 151936, 4096
+    bits, rec = tn.synthetic_record(n, k, 4, seed=151936)
+    lin = make_linear(te, bits, rec, gpu_device)
+    x = np.random.default_rng(batch).standard_normal((batch, k)).astype(np.float16)
+    y = lin(torch.from_numpy(x).to(gpu_device)).cpu().numpy()
+    for ob in (0, 255, 256, (n // 128) // 2, n // 128 - 1):
+        want = _oracle_block_rows(bits, rec, ob, x)
+        assert tn.rel_err(y[:, ob * 128:(ob + 1) * 128], want) < TOL
+        for b in range(batch):
+            assert tn.rel_err(y[b, ob * 128:(ob + 1) * 128], want[b]) < TOL
+
+
 @pytest.mark.parametrize("batch", [1, 2, 5, 40])
 def test_group_matches_single_and_oracle(te, gpu_device, batch):
     """One grouped launch of q/k/v-like and odd-shaped members equals the oracle per

@@ -132,7 +132,7 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
   // flight is static and each wait covers only the loads it needs), and per-lane offsets
   // are fixed while the per-stage part is one add. Order: output scales of the block
   // (used at the end), the fold's inputs (chunks w and w + GEMV_WAVES of the k-range),
-  // then the first NS stages of packed words.
+  // then the wave's first stage of packed words (the rest of its ring after the fold).
   const rsrc_t r_sv = make_rsrc(m.sv + ob * 128, rows * 4);
   const rsrc_t r_osc = make_rsrc(m.osc + ob * 128, rows * 4);
   const int xsh = g.x_f16 ? 1 : 2;                   // log2 bytes per activation
