@@ -240,6 +240,23 @@ def test_prefill_vs_oracle(te, gpu_device, n, k, batch):
         assert tn.rel_err(y[b], want[b]) < TOL
 
 
+@pytest.mark.parametrize("n,k,batch", [(256, 2048, 4096), (384, 1024, 2500)])
+def test_long_prefill_vs_oracle(te, gpu_device, n, k, batch):
+    """Long prefills: thousands of x-fold jobs and tens of column blocks in one launch (a
+    ragged last one at 2500), both MFMA modes, every row against the oracle."""
+    _say(f"[long prefill] n={n} k={k} batch={batch}")
+    bits, rec, W = _record_and_w_hat(n, k, 3, "mcg")
+    lin = make_linear(te, bits, rec, gpu_device)
+    x = np.random.default_rng(batch).standard_normal((batch, k)).astype(np.float16)
+    want = x.astype(np.float64) @ W.T
+    xt = torch.from_numpy(x).to(gpu_device)
+    for f16 in (False, True):
+        y = lin(xt, mma_f16=f16).cpu().numpy()
+        assert tn.rel_err(y, want) < TOL, f16
+        worst = max(tn.rel_err(y[b], want[b]) for b in range(batch))
+        assert worst < TOL, (f16, worst)
+
+
 @pytest.mark.parametrize("K,cb,V", [(2, "mcg", 1), (3, "mcg", 1), (4, "mcg", 1), (3, "3inst", 2),
                                     (3, "1mad", 1), (4, "3inst", 1), (2, "1mad", 2)])
 def test_prefill_column_block_width(te, gpu_device, monkeypatch, K, cb, V):
