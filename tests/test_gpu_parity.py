@@ -115,17 +115,23 @@ def test_linear_vs_oracle(te, gpu_device, n, k, K, cb, batch):
 
 @pytest.mark.parametrize("xdt,ydt", [(torch.float32, torch.float32), (torch.float16, torch.float16),
                                      (torch.float32, torch.float16)])
-def test_dtypes_and_strides(te, gpu_device, xdt, ydt):
-    _say(f"[linear dtypes] x={xdt} y={ydt}")
+@pytest.mark.parametrize("batch", [4, 40, 130])
+def test_dtypes_and_strides(te, gpu_device, xdt, ydt, batch):
+    """Strided rows (input stride k + 64, output stride n + 32) in every dtype pair, through
+    the decode-GEMV (4 rows) and the batched path (40 rows: one ragged 64-column block; 130:
+    several column blocks), whose x fold and output fold address rows by the strides."""
+    _say(f"[linear dtypes] x={xdt} y={ydt} batch={batch}")
     n, k = 512, 1024
     bits, rec = tn.synthetic_record(n, k, 3, seed=11)
     lin = make_linear(te, bits, rec, gpu_device)
-    xs = np.random.default_rng(0).standard_normal((4, k + 64)).astype(np.float32)
+    xs = np.random.default_rng(batch).standard_normal((batch, k + 64)).astype(np.float32)
     xt = torch.from_numpy(xs).to(gpu_device).to(xdt)[:, :k]      # row stride k+64
-    out = torch.zeros((4, n + 32), dtype=ydt, device=gpu_device)[:, :n]
+    out = torch.zeros((batch, n + 32), dtype=ydt, device=gpu_device)[:, :n]
     lin.forward(xt, out=out)
     want = tn.packed_linear_ref(bits, rec, xt.float().cpu().numpy())
     assert tn.rel_err(out.float().cpu().numpy(), want) < (2e-3 if ydt == torch.float16 else TOL)
+    # the padding columns of the output rows are never written
+    assert torch.count_nonzero(out.as_strided((batch, 32), (n + 32, 1), n)).item() == 0
 
 
 def test_repeat_calls_deterministic_and_ticket_reset(te, gpu_device):
