@@ -37,7 +37,7 @@ def make_linear(te, bits, rec, device):
     return te.PackedLinear(r, device=device)
 
 
-@functools.lru_cache(maxsize=8)
+@functools.lru_cache(maxsize=16)     # every case of CASES (pytest runs them batch by batch)
 def _case(n, k, K, cb, V):
     bits, rec = tn.synthetic_record(n, k, K, seed=7 * n + k + 3 * K + V, codebook=cb, V=V)
     zt = tn.decode_packed_tiles(bits, K, cb, V)

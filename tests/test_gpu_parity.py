@@ -92,7 +92,9 @@ def test_linear_golden_synth(te, gpu_device, K, cb):
     assert tn.rel_err(y, d["y_ref"]) < TOL
 
 
-@functools.lru_cache(maxsize=4)
+# pytest runs the parametrized cases batch by batch across the shapes, so the cache holds
+# every shape of a test (the largest W_hat, 2048 x 6144 float64, is 100 MB)
+@functools.lru_cache(maxsize=16)
 def _record_and_w_hat(n, k, K, cb):
     bits, rec = tn.synthetic_record(n, k, K, seed=n * 3 + k + K, codebook=cb)
     return bits, rec, tn.w_hat_from_record(bits, rec)
@@ -340,13 +342,18 @@ def test_v2_decode_tiles_bit_exact(te, gpu_device, K, cb):
     assert np.array_equal(sub.view(np.uint32), want[333:374].view(np.uint32))
 
 
+@functools.lru_cache(maxsize=4)
+def _v2_record_and_w_hat(n, k, K, cb):
+    bits, rec = tn.synthetic_record(n, k, K, seed=n + k + K, codebook=cb, V=2)
+    return bits, rec, tn.w_hat_from_record(bits, rec)
+
+
 @pytest.mark.parametrize("n,k,K,cb", [(256, 512, 3, "mcg"), (1536, 576, 2, "3inst"),
                                       (384, 2048, 4, "1mad"), (2048, 4096, 3, "mcg")])
 @pytest.mark.parametrize("batch", [1, 2, 3, 5, 64])
 def test_v2_linear_vs_oracle(te, gpu_device, n, k, K, cb, batch):
     _say(f"[v2 linear] n={n} k={k} K={K} cb={cb} batch={batch}")
-    bits, rec = tn.synthetic_record(n, k, K, seed=n + k + K, codebook=cb, V=2)
-    W = tn.w_hat_from_record(bits, rec)
+    bits, rec, W = _v2_record_and_w_hat(n, k, K, cb)
     lin = make_linear(te, bits, rec, gpu_device)
     x = np.random.default_rng(batch).standard_normal((batch, k)).astype(np.float16)
     y = lin(torch.from_numpy(x).to(gpu_device)).cpu().numpy()
