@@ -263,12 +263,12 @@ GroupPlan group_plan(const trellis_desc* const* W, int count, int batch, bool f1
   p.nc = bgemm_nc(W, count, batch, f16);
   p.ncb = p.gemv ? 1 : (batch + 16 * p.nc - 1) / (16 * p.nc);
   p.kr = p.gemv ? gemv_kr(W, count, batch) : bgemm_kr(W, count, batch, p.nc, f16);
-  // tiles per decode-GEMV stage: 16, or 8 for short k-ranges and for batch-1 launches that
-  // split k (a workgroup's first stage lands sooner: ~0.2 us per q/k/v and down launch of
-  // the 8B block)
+  // tiles per decode-GEMV stage: 16, or 8 for short k-ranges and for launches that split k
+  // (a workgroup's first stage lands sooner: the 8B block's q/k/v and down launches
+  // 0.2-0.7 us faster each at batch 1 to 8)
   bool split = false;
   for (int i = 0; i < count; ++i) split = split || W[i]->k_in / 16 > p.kr;
-  p.kc = p.kr >= 32 && !(p.gemv && batch == 1 && split) ? 16 : 8;
+  p.kc = p.kr >= 32 && !(p.gemv && split) ? 16 : 8;
   {
     const int kc = env_int("TRELLIS_GEMV_KC", 0);
     if (p.gemv && (kc == 8 || kc == 16) && kc <= p.kr) p.kc = kc;
