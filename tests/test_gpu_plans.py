@@ -19,7 +19,7 @@ SHAPES = [(128, 256), (256, 512), (384, 768), (640, 1024), (1024, 1536), (1536, 
 BATCHES = [1, 2, 3, 4, 5, 7, 9, 15, 16, 17, 31, 33, 63, 64, 65, 100, 127, 128, 129, 200, 257]
 
 
-def _cases(count=30, seed=2026):
+def _cases(count=60, seed=2026):
     rng = np.random.default_rng(seed)
     out = []
     for i in range(count):
