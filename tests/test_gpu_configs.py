@@ -87,10 +87,11 @@ def _check_members(te, names, K, V, batch, device, seed):
         assert (a - rhs).abs().max().item() / rhs.abs().max().item() < TOL, nm
 
 
-@pytest.mark.parametrize("batch", [16, 64])
+@pytest.mark.parametrize("batch", [2, 4, 8, 16, 64])
 @pytest.mark.parametrize("gname,names", GROUPS_8B)
 def test_qwen3_8b_block_batched(te, gpu_device, batch, gname, names):
-    """The 8B block's four launches at decode batch 16 and 64, K=3 MCG V=1."""
+    """The 8B block's four launches at decode batch 2, 4, 8 (the decode-GEMV with the rows in
+    its MFMA columns; at 8, gate+up on the batched path), 16 and 64, K=3 MCG V=1."""
     _say(f"[8B block] {gname} batch={batch}")
     _check_members(te, names, 3, 1, batch, gpu_device, seed=batch + len(gname))
 
