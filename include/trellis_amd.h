@@ -56,7 +56,8 @@ typedef enum trellis_status {
   TRELLIS_ERR_LAUNCH = 13,     /* the HIP runtime rejected a launch */
   TRELLIS_ERR_GROUP = 14,      /* group of 0 or more than 8 linears, or mixed K / V / codebook */
   TRELLIS_ERR_FLAGS = 15,      /* unknown bits in the flags of an _ex call */
-  TRELLIS_ERR_SCRATCH = 16     /* a _noalloc call needs more than TRELLIS_NOALLOC_SCRATCH_BYTES */
+  TRELLIS_ERR_SCRATCH = 16,    /* a _noalloc call needs more than TRELLIS_NOALLOC_SCRATCH_BYTES */
+  TRELLIS_ERR_CAPTURE = 17     /* the first _noalloc call on a device made under stream capture */
 } trellis_status;
 
 /* Flags of trellis_packed_linear_ex / trellis_packed_linear_group_ex. */
@@ -152,7 +153,9 @@ int trellis_packed_linear_group_ex(const trellis_desc *const *W, int count,
  * batch of 128 rows). Every call on a GPU shares that GPU's array: the split-K counters a
  * call needs are zeroed by a small kernel at its start, and calls that overlap on one GPU
  * (on different streams, or from several threads) race and must be serialized by the
- * caller. */
+ * caller. The first call on each device looks up that device's address of the array
+ * (hipGetSymbolAddress); it must not be made under stream capture, and returns
+ * TRELLIS_ERR_CAPTURE if it is. Later calls may be captured. */
 #define TRELLIS_NOALLOC_SCRATCH_BYTES (32u << 20)
 int trellis_packed_linear_group_noalloc(const trellis_desc *const *W, int count,
                                         const void *const *x, const int64_t *ldx, int batch,

@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol(te):
 
 def test_strerror_names_every_status(te):
     lib = te.library()
-    for code in range(0, 17):
+    for code in range(0, 18):
         assert lib.trellis_strerror(code).decode() not in ("", "unknown trellis status")
     assert lib.trellis_strerror(99).decode() == "unknown trellis status"
 

@@ -90,3 +90,43 @@ def test_noalloc_refuses_a_plan_beyond_the_scratch(te, gpu_device):
     assert e.value.status == 16
     assert torch.count_nonzero(y).item() == 0
     _check(te, cases, grp, 1, np.random.default_rng(5), gpu_device)
+
+
+@pytest.mark.parametrize("batch", [1, 64])
+def test_noalloc_inside_a_captured_graph(te, gpu_device, batch):
+    """noalloc calls captured in a HIP graph (after an eager first call on the device, which
+    looks up the scratch address outside the capture): at batch 1 the graph holds the
+    ticket-clearing kernel and the split-K decode-GEMV, at 64 the x fold, the batched kernel
+    and its split-K fold. Every replay, with new inputs copied in and eager noalloc calls on
+    the same scratch between replays, equals the eager call bit for bit."""
+    _say(f"[noalloc] graph capture batch={batch}")
+    cases, grp = _group(te, [(1024, 2048), (256, 2048), (384, 2048)], 800, gpu_device)
+    rng = np.random.default_rng(900 + batch)
+    xs = [torch.from_numpy(rng.standard_normal((batch, rec.k)).astype(np.float16)).to(gpu_device)
+          for _, rec, _ in cases]
+    ys = [torch.empty((batch, rec.n), device=gpu_device) for _, rec, _ in cases]
+    _noalloc(te, grp, xs, ys)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream(device=gpu_device)
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        _noalloc(te, grp, xs, ys)
+    torch.cuda.current_stream().wait_stream(side)
+    with torch.cuda.graph(g):
+        _noalloc(te, grp, xs, ys)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        xin = [torch.from_numpy(rng.standard_normal((batch, rec.k)).astype(np.float16)).to(gpu_device)
+               for _, rec, _ in cases]
+        for x, v in zip(xs, xin):
+            x.copy_(v)
+        g.replay()
+        torch.cuda.synchronize()
+        got = [y.clone() for y in ys]
+        want = [torch.empty_like(y) for y in ys]
+        _noalloc(te, grp, xin, want)
+        torch.cuda.synchronize()
+        for (bits, rec, _), a, b, v in zip(cases, got, want, xin):
+            assert torch.equal(a, b), f"replay {rep}"
+            assert tn.rel_err(a.cpu().numpy(), tn.packed_linear_ref(bits, rec, v.cpu().numpy())) < TOL

@@ -23,6 +23,7 @@ STATUS_NAMES = {
     8: "TRELLIS_ERR_ALIGN", 9: "TRELLIS_ERR_DTYPE", 10: "TRELLIS_ERR_WORKSPACE",
     11: "TRELLIS_ERR_BATCH", 12: "TRELLIS_ERR_RANGE", 13: "TRELLIS_ERR_LAUNCH",
     14: "TRELLIS_ERR_GROUP", 15: "TRELLIS_ERR_FLAGS", 16: "TRELLIS_ERR_SCRATCH",
+    17: "TRELLIS_ERR_CAPTURE",
 }
 
 # TRELLIS_NOALLOC_SCRATCH_BYTES: the static workspace of trellis_packed_linear_group_noalloc

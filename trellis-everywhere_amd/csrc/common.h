@@ -89,12 +89,15 @@ __device__ __forceinline__ void wait_vmcnt() {
 // tell which LDS bytes such a load writes, and puts a wait for every outstanding load in
 // front of each later LDS read; the caller waits for these loads itself (s_waitcnt vmcnt).
 // Loads complete in issue order, so the compiler's own waits for earlier loads stay
-// correct (they may wait longer than needed, never shorter).
+// correct (they may wait longer than needed, never shorter). GFX9 needs one wait state
+// between an SALU write of M0 and an LDS-DMA load that reads it; the compiler's hazard
+// pass does not look inside inline assembly, so the s_nop is written here.
 __device__ __forceinline__ void load_lds16(rsrc_t r, unsigned lds_base, unsigned voff) {
   unsigned saved;
   asm volatile(
       "s_mov_b32 %0, m0\n\t"
       "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
       "buffer_load_dwordx4 %2, %3, 0 offen nt lds\n\t"
       "s_mov_b32 m0, %0"
       : "=&s"(saved)

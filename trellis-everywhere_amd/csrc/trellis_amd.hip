@@ -273,6 +273,9 @@ GroupPlan group_plan(const trellis_desc* const* W, int count, int batch, bool f1
     const int kc = env_int("TRELLIS_GEMV_KC", 0);
     if (p.gemv && (kc == 8 || kc == 16) && kc <= p.kr) p.kc = kc;
   }
+  // 16 rows: two 16-tile ring slots do not fit beside the rows' activations, so the
+  // kernel's stages are 8 tiles; the plan says so too
+  if (p.gemv && gemv_nb(batch) == 16) p.kc = 8;
   p.total = 0;
   p.folds = 0;
   // Workspace: a header of counters whose layout depends only on the members' shapes (one
@@ -435,6 +438,9 @@ const char* trellis_strerror(int status) {
     case TRELLIS_ERR_SCRATCH:
       return "the call needs more workspace than the no-allocation entry point's static scratch "
              "(TRELLIS_NOALLOC_SCRATCH_BYTES)";
+    case TRELLIS_ERR_CAPTURE:
+      return "the first no-allocation call on a device must not be made under stream capture "
+             "(it looks up the device's scratch address)";
     default: return "unknown trellis status";
   }
 }
@@ -559,12 +565,16 @@ std::mutex g_scratch_mu;
 void* g_scratch_dev[MAX_DEVICES] = {};
 
 // The current device's address of `scratch`, looked up once per device (that device
-// current) and kept.
-int scratch_ptr(void** out) {
+// current) and kept. The look-up may load the code object, which is not a stream-ordered
+// operation: a first call under stream capture is refused instead (TRELLIS_ERR_CAPTURE).
+int scratch_ptr(hipStream_t st, void** out) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return TRELLIS_ERR_LAUNCH;
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch_dev[dev]) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+      return TRELLIS_ERR_CAPTURE;
     void* p = nullptr;
     if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return TRELLIS_ERR_LAUNCH;
     g_scratch_dev[dev] = p;
@@ -604,7 +614,7 @@ int packed_linear_group(const trellis_desc* const* W, int count, const void* con
   const GroupPlan p = group_plan(W, count, batch, f16);
   if (noalloc) {
     if (p.ws > NOALLOC_SCRATCH_BYTES) return TRELLIS_ERR_SCRATCH;
-    v = scratch_ptr(&workspace);
+    v = scratch_ptr(static_cast<hipStream_t>(stream), &workspace);
     if (v) return v;
     ws_bytes = NOALLOC_SCRATCH_BYTES;
   }

@@ -31,17 +31,24 @@ def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+def _ws_size(need: int) -> int:
+    """Bytes of a new workspace for `need`: the next power of two (at least 256), so a run
+    of growing batch sizes replaces the buffer O(log n) times and the retired buffers
+    together stay smaller than the current one."""
+    return 1 << max(8, (int(need) - 1).bit_length())
+
+
 def _grow_workspace(owner, need: int) -> torch.Tensor:
     """The owner's workspace, replaced by a larger zero-filled one when `need` exceeds it
     (every call leaves its counters at zero again, so a workspace is zero-filled once).
     A replaced buffer is kept alive with its owner, never freed: a HIP graph captured
     earlier still holds its address, and its replays write split-K partials and counters
     there; released to the caching allocator, that memory could belong to another tensor
-    by the next replay."""
+    by the next replay. Sizes grow geometrically (_ws_size), which bounds what is kept."""
     if owner._ws is None or owner._ws.numel() < need:
         if owner._ws is not None:
             owner._ws_retired.append(owner._ws)
-        owner._ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=owner.device)
+        owner._ws = torch.zeros(_ws_size(need), dtype=torch.uint8, device=owner.device)
     return owner._ws
 
 
