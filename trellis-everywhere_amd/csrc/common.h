@@ -25,31 +25,40 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
-struct LinMat {
+// Launch arguments. The kernels read them straight from the kernel-argument segment, which is
+// cold at every launch of a rotated weight set (~0.5-1 us a round trip): the fields a
+// kernel's first instructions need of a matrix (its first work item and what locates the
+// item, the pointers of the first loads) sit in the matrix's first 64-byte line, and the
+// launch-wide fields in the first line of all.
+struct alignas(64) LinMat {
+  // ---- first line: item location and the pointers of the first loads
+  int item0;            // first group-wide work item of this matrix
+  int S;                // k-ranges (slices)
+  unsigned s_inv;       // ceil(2^32 / S) for S > 1 (item / S = umulhi(item, s_inv)), else 0
+  int tiles_in;
   const uint32_t* bits;
-  const float* su;
-  const float* sv;
-  const float* isc;     // isc_scaled = f32(isc) * scale
-  const float* osc;
   const void* x;
-  void* y;
-  uint32_t* xf;         // workspace: [batch][xfw words] folded activations (xfold_kernel)
-  float* part;          // workspace: split-K partial sums (S > 1)
-  unsigned* tickets;    // workspace: [n_ob] arrival counters (batch 1, S > 1), zero between calls
-  long long ldx, ldy;
-  int n, k, tiles_in, block_in, block_out;
+  const float* su;
+  const float* isc;     // isc_scaled = f32(isc) * scale
+  const float* sv;
+  const float* osc;
+  // ---- second line
+  int n, block_in, k, block_out;
+  float nrm_in, nrm_out;  // 1 / sqrt(block_in), 1 / sqrt(block_out), rounded as fp32 ops
+  int n_ob;
   int xfw;              // words per xf row: k ((x, x) fp16 pairs), or kp / 2 in the fp16-weight
                         // mode (kp = k rounded up to 32; fp16 values, tile pairs interleaved)
-  float nrm_in, nrm_out;  // 1 / sqrt(block_in), 1 / sqrt(block_out), rounded as fp32 ops
-  int n_ob, S;
-  unsigned s_inv;       // ceil(2^32 / S) for S > 1 (item / S = umulhi(item, s_inv)), else 0
-  int item0;            // first group-wide work item of this matrix
+  long long ldx, ldy;
+  void* y;
+  float* part;          // workspace: split-K partial sums (S > 1)
+  // ---- third line
+  unsigned* tickets;    // workspace: [n_ob] arrival counters (batch 1, S > 1), zero between calls
+  uint32_t* xf;         // workspace: [batch][xfw words] folded activations (xfold_kernel)
   int chunk0;           // first group-wide x-fold job of this matrix
   int fold0;            // first group-wide bfold_kernel job of this matrix
 };
 
-struct LinArgs {
-  LinMat m[MAX_GROUP];
+struct alignas(64) LinArgs {
   int nmat;
   int total;            // work items of the launched kernel
   int nwords;
@@ -57,6 +66,7 @@ struct LinArgs {
   int x_f16, y_f16;
   int kr;               // tile columns per k-range
   int mma_f16;          // batched path: codebook values rounded to fp16, one MAC per weight
+  LinMat m[MAX_GROUP];
 };
 
 // Range-checked buffer loads: a buffer resource over [base, base + bytes); an offset at or

@@ -104,12 +104,29 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
   __shared__ unsigned ticket_sh;        // split-K ticket, shared with every wave (NB > 4)
   // the wave index is uniform: kept scalar, so per-wave choices are scalar branches
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  // The kernel arguments are cold at every launch of a rotated weight set (~0.5-1 us a round
+  // trip). One round of loads finds the item's matrix; every field the first loads need is
+  // then read in one second round (the empty asm that takes them all keeps the compiler from
+  // issuing them one at a time, each behind its own wait), both before the start-up barrier.
+  const int mi = locate_mat(g, blockIdx.x, false);
+  const LinMat& m = g.m[mi];
+  {
+    const int f_i0 = m.item0, f_s = m.S, f_t = m.tiles_in, f_n = m.n, f_bi = m.block_in;
+    const unsigned f_si = m.s_inv;
+    const uint32_t* f_b = m.bits;
+    const void* f_x = m.x;
+    const float *f_su = m.su, *f_is = m.isc, *f_sv = m.sv, *f_os = m.osc;
+    const long long f_ldx = m.ldx;
+    const float f_nrm = m.nrm_in;
+    const int f_kr = g.kr, f_xh = g.x_f16, f_bt = g.batch;
+    asm volatile("" ::"s"(f_i0), "s"(f_s), "s"(f_t), "s"(f_n), "s"(f_bi), "s"(f_si), "s"(f_b),
+                 "s"(f_x), "s"(f_su), "s"(f_is), "s"(f_sv), "s"(f_os), "s"(f_ldx), "s"(f_nrm),
+                 "s"(f_kr), "s"(f_xh), "s"(f_bt));
+  }
   if (threadIdx.x < KRM / 8) ready[threadIdx.x] = 0u;
   if (threadIdx.x == 0) nready = 0u;
   __syncthreads();
   const int bl = wave & 7, half = wave >> 3;     // band of the block, half of the k-range
-  const int mi = locate_mat(g, blockIdx.x, false);
-  const LinMat& m = g.m[mi];
   const unsigned local = blockIdx.x - m.item0;
   const int ob = m.S > 1 ? static_cast<int>(__umulhi(local, m.s_inv)) : static_cast<int>(local);
   const int sl = static_cast<int>(local) - ob * m.S;
