@@ -1,10 +1,12 @@
 """GPU parity at the benchmark workloads themselves, through the launches bench.py times.
 
-* Qwen3-8B block linears at decode batch 16 and 64: q/k/v as one PackedGroup, o, gate/up as
-  one PackedGroup, down, i.e. the exact plans of the bench (16-row decode-GEMV and batched
-  kernel at 16; batched kernel with split-K fold at 64).
-* The bit-rate sweep on the 8B gate/up/down shapes (4096 <-> 12288): K = 2, 4 x V = 1, 2 at
-  batch 1, and a 512-token prefill at K = 3 V = 1, K = 2 V = 1 and K = 3 V = 2.
+* Qwen3-8B block linears at decode batch 1 (the headline: the q/k/v group's split-K
+  decode-GEMV over 240 items, gate+up as one launch of 192 whole blocks), 2, 4, 8, 16 and 64:
+  q/k/v as one PackedGroup, o, gate/up as one PackedGroup, down, i.e. the exact plans of the
+  bench (decode-GEMV up to 16 rows, the batched kernel for gate+up at 8 and 16 and for
+  every launch at 64, with its split-K fold).
+* Every point of the bit-rate sweep on the 8B gate/up/down shapes (4096 <-> 12288): K = 2,
+  3, 4 x V = 1, 2 at batch 1 and at a 512-token prefill.
 
 A dense float64 oracle of a whole 8B matrix (50M weights) would take minutes, so three
 128-row output blocks (first, middle, last) of every member are checked against the oracle
@@ -87,24 +89,26 @@ def _check_members(te, names, K, V, batch, device, seed):
         assert (a - rhs).abs().max().item() / rhs.abs().max().item() < TOL, nm
 
 
-@pytest.mark.parametrize("batch", [2, 4, 8, 16, 64])
+@pytest.mark.parametrize("batch", [1, 2, 4, 8, 16, 64])
 @pytest.mark.parametrize("gname,names", GROUPS_8B)
 def test_qwen3_8b_block_batched(te, gpu_device, batch, gname, names):
-    """The 8B block's four launches at decode batch 2, 4, 8 (the decode-GEMV with the rows in
-    its MFMA columns; at 8, gate+up on the batched path), 16 and 64, K=3 MCG V=1."""
+    """The 8B block's four launches at decode batch 1 (the headline plans), 2, 4, 8 (the
+    decode-GEMV with the rows in its MFMA columns; at 8, gate+up on the batched path), 16 and
+    64, K=3 MCG V=1."""
     _say(f"[8B block] {gname} batch={batch}")
     _check_members(te, names, 3, 1, batch, gpu_device, seed=batch + len(gname))
 
 
-@pytest.mark.parametrize("K,V", [(2, 1), (4, 1), (2, 2), (4, 2)])
+@pytest.mark.parametrize("K,V", [(2, 1), (4, 1), (2, 2), (3, 2), (4, 2)])
 @pytest.mark.parametrize("gname,names", [("gate_up", ("gate", "up")), ("down", ("down",))])
 def test_sweep_batch1(te, gpu_device, K, V, gname, names):
-    """The bit-rate sweep's batch-1 points on the 8B gate/up/down shapes."""
+    """The bit-rate sweep's batch-1 points on the 8B gate/up/down shapes (K=3 V=1 is the
+    headline block's own gate+up and down, above)."""
     _say(f"[sweep] {gname} K={K} V={V} batch=1")
     _check_members(te, names, K, V, 1, gpu_device, seed=10 * K + V)
 
 
-@pytest.mark.parametrize("K,V", [(3, 1), (2, 1), (3, 2)])
+@pytest.mark.parametrize("K,V", [(3, 1), (2, 1), (3, 2), (2, 2), (4, 1), (4, 2)])
 @pytest.mark.parametrize("gname,names", [("gate_up", ("gate", "up")), ("down", ("down",))])
 def test_sweep_prefill512(te, gpu_device, K, V, gname, names):
     """The bit-rate sweep's 512-token prefill points on the 8B gate/up/down shapes."""
