@@ -39,20 +39,17 @@ namespace trellis {
 // columns w, w + WAVES, ..: all of them at once, level by level (fwht_chunks), so their
 // lane exchanges overlap (one column after another, the fold of 64 columns measured ~2 us
 // at the end of every batched launch); a wave's slots past nbv repeat column nbv - 1 and
-// are not stored.
+// are not stored. so[h] = sv * osc of row 128 ob + min(lane + 64 h, rows - 1), loaded by
+// the caller long before (cold, their load took ~1 us when the fold issued it).
 template <int CB, int WAVES, int TLS, int NR, int NR_OFF, int NB>
 __device__ __forceinline__ void bg_out_fold(const LinArgs& g, const LinMat& m, const float* tl,
-                                            int ob, int b0, int nbv, int rows) {
+                                            int ob, int b0, int nbv, int rows,
+                                            const float (&sov)[2]) {
   constexpr int C = (NB + WAVES - 1) / WAVES;   // columns per wave
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   if (wave >= nbv) return;
   const float nrm = m.nrm_out;
-  float so[2];
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int row = ob * 128 + min(lane + 64 * h, rows - 1);
-    so[h] = m.sv[row] * m.osc[row] * nrm;
-  }
+  const float so[2] = {sov[0] * nrm, sov[1] * nrm};
   const FwhtLane fl = fwht_lane(lane, m.block_out);
   float lo[C], hi[C];
 #pragma unroll
@@ -112,6 +109,14 @@ template <int NC, int F16> struct BgBands {
   static constexpr int BW = (!F16 && NC == 1) ? 4 : 2;
 };
 
+// s_setprio with a value known after unrolling (the instruction takes an immediate)
+__device__ __forceinline__ void setprio_n(int v) {
+  if (v >= 3) __builtin_amdgcn_s_setprio(3);
+  else if (v == 2) __builtin_amdgcn_s_setprio(2);
+  else if (v == 1) __builtin_amdgcn_s_setprio(1);
+  else __builtin_amdgcn_s_setprio(0);
+}
+
 template <int K, int CB, int V, int NC, int F16>
 __global__ __launch_bounds__((64 * BgWaves<NC, F16>::WV)) void bgemm_kernel(LinArgs g) {
   constexpr int BG_WAVES = BgWaves<NC, F16>::WV;
@@ -150,6 +155,16 @@ __global__ __launch_bounds__((64 * BgWaves<NC, F16>::WV)) void bgemm_kernel(LinA
   const int bg = wave % NG, kl = wave / NG;
   const int mi = locate_mat(g, blockIdx.x, false);
   const LinMat& m = g.m[mi];
+  {
+    // the matrix's fields that the set-up needs, loaded in one round (the argument segment
+    // is cold; used one by one, the loads would go out in several dependent rounds)
+    const int f_i0 = m.item0, f_s = m.S, f_t = m.tiles_in, f_n = m.n, f_xw = m.xfw;
+    const int f_bt = g.batch, f_kr = g.kr;
+    const uint32_t *f_b = m.bits, *f_xf = m.xf;
+    const float *f_sv = m.sv, *f_os = m.osc;
+    asm volatile("" ::"s"(f_i0), "s"(f_s), "s"(f_t), "s"(f_n), "s"(f_xw), "s"(f_bt), "s"(f_kr),
+                 "s"(f_b), "s"(f_xf), "s"(f_sv), "s"(f_os));
+  }
   const int local = blockIdx.x - m.item0;
   const int ncb = (g.batch + NB - 1) / NB;
   const int sl = local % m.S, obcb = local / m.S;
@@ -212,6 +227,16 @@ __global__ __launch_bounds__((64 * BgWaves<NC, F16>::WV)) void bgemm_kernel(LinA
     }
   };
 
+  // one k-range: the output fold's scales, loaded now so their latency hides behind the loop
+  float sov[2] = {0.f, 0.f};
+  if (m.S == 1) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int row = ob * 128 + min(lane + 64 * h, rows - 1);
+      sov[h] = m.sv[row] * m.osc[row];
+    }
+  }
+
   const int r = lane & 15, gq = lane >> 4;
   const QuadPos qp = quad_pos_v<K, V>(r, gq);
   float4_t acc[BW][NC];
@@ -224,6 +249,7 @@ __global__ __launch_bounds__((64 * BgWaves<NC, F16>::WV)) void bgemm_kernel(LinA
   load_step(1, xr[1], br[1]);
   store_b(0, xr[0]);
   __syncthreads();
+  __builtin_amdgcn_s_setprio(3);
   // two steps per trip so the register rings keep a fixed shape; a step past the last
   // computes nothing, and its loads read nothing
   for (int s = 0; s < nsteps; s += 2) {
@@ -248,16 +274,35 @@ __global__ __launch_bounds__((64 * BgWaves<NC, F16>::WV)) void bgemm_kernel(LinA
           if (st * KT + 2 * kl < ntl) {
             const uint32_t* p0 = mystg;                 // band 2bg: tiles 2kl, 2kl + 1
             const uint32_t* p1 = mystg + TPL * NWK;     // band 2bg + 1
-            const half8_t A0 = decode_a_pair<K, CB, V>(p0[qp.wa], p0[qp.wb], p0[NWK + qp.wa],
-                                                       p0[NWK + qp.wb], qp.sh);
-            const half8_t A1 = decode_a_pair<K, CB, V>(p1[qp.wa], p1[qp.wb], p1[NWK + qp.wa],
-                                                       p1[NWK + qp.wb], qp.sh);
+            // the window words and the first two fragments are read before the decode, and
+            // each later pair of fragments while the MFMAs of the pair before it run (read
+            // just before its own MFMAs, each pair's LDS latency was exposed)
+            const uint32_t w0a = p0[qp.wa], w0b = p0[qp.wb], w0c = p0[NWK + qp.wa], w0d = p0[NWK + qp.wb];
+            const uint32_t w1a = p1[qp.wa], w1b = p1[qp.wb], w1c = p1[NWK + qp.wa], w1d = p1[NWK + qp.wb];
+            constexpr int FP = NC < 2 ? NC : 2;         // fragments per group
+            auto frag = [&](int c) {
+              return __builtin_bit_cast(half8_t, *reinterpret_cast<const u32x4_t*>(xb + c * 16 * XW + kl * 16));
+            };
+            half8_t Bn[FP];
 #pragma unroll
-            for (int c = 0; c < NC; ++c) {
-              const half8_t B = __builtin_bit_cast(
-                  half8_t, *reinterpret_cast<const u32x4_t*>(xb + c * 16 * XW + kl * 16));
-              acc[0][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, B, acc[0][c], 0, 0, 0);
-              acc[1][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, B, acc[1][c], 0, 0, 0);
+            for (int f = 0; f < FP; ++f) Bn[f] = frag(f);
+            const half8_t A0 = decode_a_pair<K, CB, V>(w0a, w0b, w0c, w0d, qp.sh);
+            const half8_t A1 = decode_a_pair<K, CB, V>(w1a, w1b, w1c, w1d, qp.sh);
+#pragma unroll
+            for (int c0 = 0; c0 < NC; c0 += FP) {
+              half8_t Bc[FP];
+#pragma unroll
+              for (int f = 0; f < FP; ++f) Bc[f] = Bn[f];
+              if (c0 + FP < NC) {
+#pragma unroll
+                for (int f = 0; f < FP; ++f) Bn[f] = frag(c0 + FP + f);
+              }
+#pragma unroll
+              for (int f = 0; f < FP; ++f) {
+                acc[0][c0 + f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, Bc[f], acc[0][c0 + f], 0, 0, 0);
+                acc[1][c0 + f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, Bc[f], acc[1][c0 + f], 0, 0, 0);
+              }
+              setprio_n(2 - 4 * (c0 + FP) / NC);
             }
           }
         } else {
@@ -289,6 +334,7 @@ __global__ __launch_bounds__((64 * BgWaves<NC, F16>::WV)) void bgemm_kernel(LinA
 #pragma unroll
                 for (int c = 0; c < NC; ++c)
                   acc[b][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bf[c], acc[b][c], 0, 0, 0);
+                setprio_n(2 - (t * BW + b) * 4 / (TPL * BW));
               }
             }
           }
@@ -296,8 +342,10 @@ __global__ __launch_bounds__((64 * BgWaves<NC, F16>::WV)) void bgemm_kernel(LinA
       }
       // every wave is done with this step's buffer, and the next step's B is stored
       __syncthreads();
+      __builtin_amdgcn_s_setprio(3);
     }
   }
+  __builtin_amdgcn_s_setprio(0);
   // the rings' last loads (steps past the end) are not consumed: let them land
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
@@ -329,7 +377,7 @@ __global__ __launch_bounds__((64 * BgWaves<NC, F16>::WV)) void bgemm_kernel(LinA
     }
     return;
   }
-  bg_out_fold<CB, BG_WAVES, TLS, NR, NR_OFF, NB>(g, m, tl, ob, b0, nbv, rows);
+  bg_out_fold<CB, BG_WAVES, TLS, NR, NR_OFF, NB>(g, m, tl, ob, b0, nbv, rows, sov);
 }
 
 // Split-K reduction of bgemm_kernel: one wave per (matrix, 128-row block, batch column):

@@ -286,20 +286,31 @@ __device__ __forceinline__ uint32_t dup_half(float v) {
   return (static_cast<uint32_t>(u) << 16) | u;
 }
 
-__device__ __forceinline__ int locate_fold(const LinArgs& g, int it) {
+// The matrix of a group-wide job number: the last one whose first job (field F of LinMat)
+// is at or below it. Every matrix's first-job field is loaded in one round, needed or not
+// (the argument segment holds all MAX_GROUP entries; conditional loads went out in two
+// dependent rounds from the cold segment).
+template <int LinMat::*F>
+__device__ __forceinline__ int locate_by(const LinArgs& g, int it) {
+  int s[MAX_GROUP];
+#pragma unroll
+  for (int j = 1; j < MAX_GROUP; ++j) s[j] = g.m[j].*F;
+  const int nm = g.nmat;
+  asm volatile("" ::"s"(s[1]), "s"(s[2]), "s"(s[3]), "s"(s[4]), "s"(s[5]), "s"(s[6]), "s"(s[7]),
+               "s"(nm));
   int mi = 0;
 #pragma unroll
   for (int j = 1; j < MAX_GROUP; ++j)
-    if (j < g.nmat && it >= g.m[j].fold0) mi = j;
+    if (j < nm && it >= s[j]) mi = j;
   return mi;
 }
 
+__device__ __forceinline__ int locate_fold(const LinArgs& g, int it) {
+  return locate_by<&LinMat::fold0>(g, it);
+}
+
 __device__ __forceinline__ int locate_mat(const LinArgs& g, int it, bool by_chunk) {
-  int mi = 0;
-#pragma unroll
-  for (int j = 1; j < MAX_GROUP; ++j)
-    if (j < g.nmat && it >= (by_chunk ? g.m[j].chunk0 : g.m[j].item0)) mi = j;
-  return mi;
+  return by_chunk ? locate_by<&LinMat::chunk0>(g, it) : locate_by<&LinMat::item0>(g, it);
 }
 
 // The fp16-weight mode's B layout: the 32 activations of a tile pair (columns 32p .. 32p+31)
