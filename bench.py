@@ -491,6 +491,28 @@ def calibration_passes(torch, dev):
     torch.cuda.empty_cache()
 
 
+def ceilings(K):
+    """What this decode allows on one MI355X, beside the targets: the batch-1 VALU floor of
+    the block (13.4 VALU operations per 16x16 tile per wave at 4 cycles each, every one of
+    the 1024 SIMDs issuing VALU every cycle at 2.4 GHz) and the batch-64 MFMA ceilings of
+    the exact mode (the (hi, lo) pair is two MACs per weight). The measured figures are
+    from microbenchmarks of this decode and of plain MFMA loops on the same GPU."""
+    tiles = sum(n * k // 256 for _, n, k in LAYERS)
+    floor_s = 13.4 * 4 * tiles / 1024 / 2.4e9
+    block_bytes = sum(n * k * K // 8 for _, n, k in LAYERS)
+    return {
+        "batch1_valu_floor_us": round(floor_s * 1e6, 2),
+        "batch1_valu_floor_pct_of_hbm_peak": round(100 * block_bytes / floor_s / 1e9
+                                                   / HBM_PEAK_GBS, 1),
+        "batch1_target_us": round(block_bytes / (0.6 * HBM_PEAK_GBS * 1e9) * 1e6, 2),
+        "batch64_exact_mode_max_pct_of_fp16_peak": 50,
+        "batch64_compute_only_loop_pct_of_fp16_peak": 35,
+        "mfma_only_sustained_clock_ghz": [1.76, 1.90],
+        "basis": "13.4 VALU ops/tile at 4 cycles on 1024 SIMDs at 2.4 GHz; exact mode = 2 "
+                 "MACs per weight; decode + 4 MFMAs per band-tile at 4 waves/SIMD without "
+                 "memory traffic: 91 cycles/band-tile, 70 % matrix busy"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -600,7 +622,8 @@ def main():
                    "batch64": batch64,
                    "prefill512": batched.get(512),
                    "sweep_configs4": sweep,
-                   "next_rows": extra},
+                   "next_rows": extra,
+                   "ceilings": ceilings(K)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_from_profile() if B == 1 and K == 3 and V == 1 else None,
