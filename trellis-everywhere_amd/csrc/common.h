@@ -323,13 +323,18 @@ __device__ __forceinline__ int xf_pair_slot(int e) {
 
 // ---------------------------------------------------------------- x fold
 // xf = Hb_k(isc * su * x) scaled by 1/sqrt(block_in), stored as (x,x) fp16 pairs. One
-// wave per (matrix, batch row, 128-column chunk), every load a range-checked buffer load
-// issued up front. The kernel is latency-bound (a few MB at most): one row per wave gives
-// every SIMD several waves to overlap the transform's dependent lane exchanges (8B gate+up
-// fold at batch 64, alone in a graph chain: 2.7 us per launch, against 2.9 with 2 rows and
-// 3.6 with 4 rows per wave). Defined in one translation unit only.
-constexpr int XFOLD_ROWS = 1;
+// wave per (matrix, group of R batch rows, 128-column chunk), every load a range-checked
+// buffer load issued up front. Up to 64 rows the kernel is latency-bound (a few MB): one
+// row per wave gives every SIMD several waves to overlap the transform's dependent lane
+// exchanges (8B gate+up fold at batch 64, alone in a graph chain: 2.7 us per launch,
+// against 2.9 with 2 rows and 3.6 with 4 rows per wave). From 256 rows up a launch needs
+// several rounds of waves on the CUs, each paying the start-up latency: four rows per wave
+// (their scales loaded once, the rows transformed together) took the 8B block's folds at
+// batch 512 from 12.5 to 9.5 us per launch on average (kernel trace), eight rows 9.7; the
+// block 517 -> 503.5 us, 360 -> 347.5 in the fp16-weight mode; at 128 rows no change.
+__host__ __device__ constexpr int xfold_rows(int batch) { return batch >= 256 ? 4 : 1; }
 #ifdef TRELLIS_XFOLD_DEFINE
+template <int XFOLD_ROWS>
 __global__ __launch_bounds__(256) void xfold_kernel(LinArgs g) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int job = blockIdx.x * 4 + wave;
@@ -358,13 +363,20 @@ __global__ __launch_bounds__(256) void xfold_kernel(LinArgs g) {
   }
   const float nrm = m.nrm_in;
   const FwhtLane fl = fwht_lane(lane, m.block_in);
+  // the rows are transformed together, level by level, so their dependent lane exchanges
+  // overlap (rows past the call's were loaded as zeros and are not stored)
+  float lov[XFOLD_ROWS], hiv[XFOLD_ROWS];
+#pragma unroll
+  for (int r = 0; r < XFOLD_ROWS; ++r) {
+    // an f16 row stride is even, so the element's half within its word follows e
+    lov[r] = lane < kvalid ? act_value(w0[r], e0, g.x_f16) * s0 : 0.0f;
+    hiv[r] = lane + 64 < kvalid ? act_value(w1[r], e1, g.x_f16) * s1 : 0.0f;
+  }
+  fwht_chunks<XFOLD_ROWS>(lov, hiv, m.block_in, lane, fl);
 #pragma unroll
   for (int r = 0; r < XFOLD_ROWS; ++r) {
     if (b0 + r >= g.batch) break;
-    // an f16 row stride is even, so the element's half within its word follows e
-    float lo = lane < kvalid ? act_value(w0[r], e0, g.x_f16) * s0 : 0.0f;
-    float hi = lane + 64 < kvalid ? act_value(w1[r], e1, g.x_f16) * s1 : 0.0f;
-    fwht_chunk(lo, hi, m.block_in, lane, fl);
+    const float lo = lov[r], hi = hiv[r];
     if (g.mma_f16) {
       // fp16 values in tile-pair order (xf_pair_slot); columns k .. kp - 1 of the last
       // pair are written as zeros (lo and hi are zero there)

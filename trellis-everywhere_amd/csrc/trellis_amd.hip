@@ -320,7 +320,10 @@ int launch_gemv(int K, int cb, int V, int kc, const LinArgs& g, hipStream_t st) 
 int launch_xfold(LinArgs& g, int folds, hipStream_t st) {
   const int items = g.total;
   g.total = folds;
-  hipLaunchKernelGGL(xfold_kernel, dim3(static_cast<unsigned>((folds + 3) / 4)), dim3(256), 0, st, g);
+  if (xfold_rows(g.batch) == 4)
+    hipLaunchKernelGGL(xfold_kernel<4>, dim3(static_cast<unsigned>((folds + 3) / 4)), dim3(256), 0, st, g);
+  else
+    hipLaunchKernelGGL(xfold_kernel<1>, dim3(static_cast<unsigned>((folds + 3) / 4)), dim3(256), 0, st, g);
   g.total = items;
   return hipGetLastError() == hipSuccess ? TRELLIS_OK : TRELLIS_ERR_LAUNCH;
 }
@@ -694,7 +697,7 @@ int packed_linear_group(const trellis_desc* const* W, int count, const void* con
       g.m[i].x = static_cast<const char*>(x[i]) + static_cast<size_t>(b0) * ldx[i] * xes;
       g.m[i].y = static_cast<char*>(y[i]) + static_cast<size_t>(b0) * ldy[i] * yes;
       g.m[i].chunk0 = chunk0;
-      chunk0 += ((g.batch + XFOLD_ROWS - 1) / XFOLD_ROWS) * ((W[i]->k_in + 127) / 128);
+      chunk0 += ((g.batch + xfold_rows(g.batch) - 1) / xfold_rows(g.batch)) * ((W[i]->k_in + 127) / 128);
     }
     v = p.gemv ? launch_gemv(W[0]->K, W[0]->codebook, W[0]->V, p.kc, g, st)
                : launch_bgemm(W[0]->K, W[0]->codebook, W[0]->V, p.nc, g, chunk0, nfold, st);
