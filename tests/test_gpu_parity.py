@@ -265,6 +265,28 @@ def test_long_prefill_vs_oracle(te, gpu_device, n, k, batch):
         assert worst < TOL, (f16, worst)
 
 
+@pytest.mark.parametrize("batch", [257, 258, 259, 262])
+def test_prefill_ragged_fold_rows(te, gpu_device, batch):
+    """From 256 rows up the x fold takes four batch rows per wave: a batch that is not a
+    multiple of four leaves the last group 1, 2 or 3 rows, whose missing rows must be
+    neither read into the result nor stored. Both MFMA modes, every row against the
+    oracle, and its first 255 rows equal to a call on those rows alone (one row per wave in
+    that call's fold; the plans may differ, so within 1e-5)."""
+    _say(f"[prefill ragged fold] batch={batch}")
+    n, k = 384, 1024
+    bits, rec, W = _record_and_w_hat(n, k, 3, "mcg")
+    lin = make_linear(te, bits, rec, gpu_device)
+    x = np.random.default_rng(batch).standard_normal((batch, k)).astype(np.float16)
+    want = x.astype(np.float64) @ W.T
+    xt = torch.from_numpy(x).to(gpu_device)
+    for f16 in (False, True):
+        y = lin(xt, mma_f16=f16).cpu().numpy()
+        worst = max(tn.rel_err(y[b], want[b]) for b in range(batch))
+        assert worst < TOL, (f16, worst)
+        head = lin(xt[:255], mma_f16=f16).cpu().numpy()
+        assert tn.rel_err(y[:255], head) < 1e-5, f16
+
+
 @pytest.mark.parametrize("K,cb,V", [(2, "mcg", 1), (3, "mcg", 1), (4, "mcg", 1), (3, "3inst", 2),
                                     (3, "1mad", 1), (4, "3inst", 1), (2, "1mad", 2)])
 def test_prefill_column_block_width(te, gpu_device, monkeypatch, K, cb, V):
