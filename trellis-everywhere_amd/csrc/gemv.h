@@ -80,6 +80,9 @@ __host__ __device__ constexpr int gemv_lds_bytes(int K, int KC, int nb) {
               gemv_kr_max(nb) / 8 + 4);
 }
 
+// rows of activations transformed together by the fold (a compile-time count for a lambda)
+template <int N> struct RowGroup { static constexpr int value = N; };
+
 template <int K, int CB, int V, int KC, int NB>
 __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
   constexpr int NWK = 8 * K;                 // words per tile
@@ -191,8 +194,9 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
       const unsigned e = ch < nch ? ch * 128 + lane + 64 * h : RSRC_OOB / 4;
 #pragma unroll
       for (int n = 0; n < NB; ++n) {
-        // batch row n of the call (rows past it, or not this wave's, read zeros)
-        const unsigned en = n >= f_r0 && n < f_r1 && ch < nch ? n * ldx + e : RSRC_OOB / 4;
+        // the wave's n-th row, batch row f_r0 + n of the call (rows past its share read zeros)
+        const int r = f_r0 + n;
+        const unsigned en = r < f_r1 && ch < nch ? r * ldx + e : RSRC_OOB / 4;
         fw[f][n][h] = __builtin_amdgcn_raw_buffer_load_b32(r_x, static_cast<int>(((en << xsh) & ~3u)), 0, 0);
       }
       fsu[f][h] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r_su, static_cast<int>(e * 4), 0, 0));
@@ -238,26 +242,39 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
         // element's half within its word follows e. Rows are transformed RG at a time,
         // level by level (fwht_chunks), so their dependent lane exchanges overlap (one row
         // after another, a wave's 16-row fold took up to ~6 us at batch 16); a group's rows
-        // that are not this wave's were loaded as zeros and are not stored.
-        constexpr int RG = NB < 8 ? NB : 8;
+        // past the wave's share were loaded as zeros and are not stored. A wave with at most
+        // four rows (16 rows over four chunks) transforms them four at a time: in groups of
+        // eight, half its fold was rows of zeros.
+        const int nr = f_r1 - f_r0;
+        auto fold_rows = [&](auto rg) {
+          constexpr int RG = decltype(rg)::value;
 #pragma unroll
-        for (int g0 = 0; g0 < NB; g0 += RG) {
-          if (g0 >= f_r1 || g0 + RG <= f_r0) continue;
-          float lo[RG], hi[RG];
+          for (int g0 = 0; g0 < NB; g0 += RG) {
+            if (g0 >= nr) continue;
+            float lo[RG], hi[RG];
 #pragma unroll
-          for (int j = 0; j < RG; ++j) {
-            lo[j] = act_value(fw[f][g0 + j][0], e0, g.x_f16) * (fsu[f][0] * fis[f][0]);
-            hi[j] = act_value(fw[f][g0 + j][1], e1, g.x_f16) * (fsu[f][1] * fis[f][1]);
-          }
-          fwht_chunks<RG>(lo, hi, m.block_in, lane, fl);
+            for (int j = 0; j < RG; ++j) {
+              lo[j] = act_value(fw[f][g0 + j][0], e0, g.x_f16) * (fsu[f][0] * fis[f][0]);
+              hi[j] = act_value(fw[f][g0 + j][1], e1, g.x_f16) * (fsu[f][1] * fis[f][1]);
+            }
+            fwht_chunks<RG>(lo, hi, m.block_in, lane, fl);
 #pragma unroll
-          for (int j = 0; j < RG; ++j) {
-            const int n = g0 + j;
-            if (n >= f_r0 && n < f_r1) {
-              xs[n * XROW + e0] = dup_half(lo[j] * nrm);
-              xs[n * XROW + e1] = dup_half(hi[j] * nrm);
+            for (int j = 0; j < RG; ++j) {
+              if (g0 + j < nr) {
+                const int n = f_r0 + g0 + j;
+                xs[n * XROW + e0] = dup_half(lo[j] * nrm);
+                xs[n * XROW + e1] = dup_half(hi[j] * nrm);
+              }
             }
           }
+        };
+        if constexpr (SPLIT) {
+          if (nr <= 4)
+            fold_rows(RowGroup<4>{});
+          else
+            fold_rows(RowGroup<8>{});
+        } else {
+          fold_rows(RowGroup<(NB < 8 ? NB : 8)>{});
         }
         // publish the chunk's rows: their xs words are written before the count
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
