@@ -7,7 +7,11 @@ fp16 N(0,1) activations, batch 1. One step = the seven packed linears of one blo
 forward order as four launches (q/k/v grouped, o, gate/up grouped, down: o waits for
 attention and down for the MLP activation in a real forward pass). Weights are resident in
 HBM; to defeat the 256 MB Infinity Cache the steps rotate over `copies` distinct blocks
-(>= 1 GB of packed bits). Each copy's four launches are one HIP graph; steps replay them.
+(>= 1 GB of packed bits). One HIP graph holds a run of blocks, one per copy (a model's
+forward pass is captured whole, so a graph launch is not charged to every block); the
+timed region replays whole runs and then a graph of the remaining blocks, exactly `steps`
+blocks. The same blocks with one graph per block (a graph launch each) are reported
+beside it ("us_per_block_one_graph_per_block").
 
 value = packed-weight bytes of the block / seconds per step (GB/s, algorithmic bytes
 n*k*K/8). The JSON line also carries us/layer, the dominant launch's HBM roofline (gate+up,
@@ -19,7 +23,7 @@ the 8B gate/up/down shapes, at batch 1 and at a 512-token prefill) runs by defau
 (--no-sweep skips it), each point with its own roofline.
 
 The CPU-baseline leg also checks what the timed launches computed: after each timed run,
-copy 0's graph is replayed once more and sampled 128-row output blocks are copied to the
+a graph of copy 0's block is replayed and sampled 128-row output blocks are copied to the
 host (three per layer, one per layer at a sweep point); the oracle's float64 W_hat @ x
 judges them at the reference's 1e-3 metric ("output_check"). A failed check prints the
 JSON line and exits with status 3. --no-cpu-baseline skips both.
@@ -139,12 +143,18 @@ def take_samples(blk, xs, ys, layers, label, per_layer):
 
 def run_block(te, torch, dev, layers, groups, B, K, V, steps, warmup, min_bytes=1.0e9,
               per_launch=True, mma_f16=False, copies=None, singles=True, samples=None,
-              label="", sample_blocks=3):
-    """Time `steps` replays of the block (its launches in order) over distinct weight copies.
-    Returns (seconds per step, {group: us per launch}, {layer: us per launch}); singles=False
-    never launches the layers one by one (a counter run then sees only the group launches).
-    With a `samples` list, copy 0's graph is replayed once more after the timed steps and
-    what its launches wrote is appended for the output check (take_samples)."""
+              label="", sample_blocks=3, graph_each=None):
+    """Time `steps` blocks (each block's launches in order) over distinct weight copies.
+    One HIP graph holds a run of blocks, one per weight copy, as a model's forward pass is
+    captured whole: a graph launch is then not charged to every block. The timed region
+    holds exactly `steps` blocks: whole runs, then a graph of the first `steps % copies`
+    copies. Returns (seconds per step, {group: us per launch}, {layer: us per launch},
+    copies); singles=False never launches the layers one by one (a counter run then sees
+    only the group launches). With a `graph_each` dict, `steps` more blocks are timed with
+    one graph per block (one graph launch per block) and their seconds per block stored
+    under "sec". With a `samples` list, a graph of copy 0's block is replayed after the
+    timed steps and what its launches wrote is appended for the output check
+    (take_samples)."""
     block_bytes = sum(n * k * K // 8 for _, n, k in layers)
     if copies is None:
         copies = max(2, math.ceil(min_bytes / block_bytes))
@@ -172,19 +182,37 @@ def run_block(te, torch, dev, layers, groups, B, K, V, steps, warmup, min_bytes=
             for name, _, _ in layers:
                 single(c, name)
     torch.cuda.synchronize()
-    graphs = [capture(torch, lambda c=c: step(c)) for c in range(copies)]
-    for s in range(warmup):
-        graphs[s % copies].replay()
+    run = capture(torch, lambda: [step(c) for c in range(copies)])
+    tail_n = steps % copies
+    tail = capture(torch, lambda: [step(c) for c in range(tail_n)]) if tail_n else None
+    for _ in range(max(1, math.ceil(warmup / copies))):
+        run.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for s in range(steps):
-        graphs[s % copies].replay()
+    for _ in range(steps // copies):
+        run.replay()
+    if tail is not None:
+        tail.replay()
     torch.cuda.synchronize()
     sec = (time.perf_counter() - t0) / steps
+    del run, tail
+    if graph_each is not None:
+        graphs = [capture(torch, lambda c=c: step(c)) for c in range(copies)]
+        for s in range(warmup):
+            graphs[s % copies].replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for s in range(steps):
+            graphs[s % copies].replay()
+        torch.cuda.synchronize()
+        graph_each["sec"] = (time.perf_counter() - t0) / steps
+        del graphs
     if samples is not None:
-        graphs[0].replay()
+        g0 = capture(torch, lambda: step(0))
+        g0.replay()
         torch.cuda.synchronize()
         samples.extend(take_samples(blocks[0], xs, ys, layers, label, sample_blocks))
+        del g0
 
     us_group, us_layer = {}, {}
     if per_launch:
@@ -210,7 +238,7 @@ def run_block(te, torch, dev, layers, groups, B, K, V, steps, warmup, min_bytes=
         if singles:
             us_layer = {name: round(per_launch_us(lambda c, name=name: single(c, name)), 3)
                         for name, _, _ in layers}
-    del graphs, grps, blocks
+    del grps, blocks
     torch.cuda.empty_cache()
     return sec, us_group, us_layer, copies
 
@@ -414,14 +442,18 @@ def batched_figure(te, torch, dev, bs, K, V, args, samples=None):
     roofline (algorithmic 2*bs*n*k flops over the launch, launch gap included)."""
     log(f"[bench] block batch {bs}")
     steps, warmup = max(20, args.steps // 10), max(3, args.warmup // 5)
-    sec, grp, _, _ = run_block(te, torch, dev, LAYERS, GROUPS, bs, K, V, steps, warmup,
-                               per_launch=True, samples=samples, label=f"block batch {bs}")
+    ge, geh = {}, {}
+    sec, grp, _, copies = run_block(te, torch, dev, LAYERS, GROUPS, bs, K, V, steps, warmup,
+                                    per_launch=True, samples=samples, label=f"block batch {bs}",
+                                    graph_each=ge)
     fl = block_flops(LAYERS, bs)
     dom_fl = 2 * bs * 2 * 12288 * 4096
     dom_tf = dom_fl / (grp[DOMINANT] * 1e-6) / 1e12
     # the planner's width for gate+up (above 64 columns: 128 here, by its cost model)
     nc = 1 if bs <= 16 else 2 if bs <= 32 else 4 if bs <= 64 else 8
     out = {"us_per_block": round(sec * 1e6, 2),
+           "us_per_block_one_graph_per_block": round(ge["sec"] * 1e6, 2),
+           "blocks_per_graph": copies,
            "tflops": round(fl / sec / 1e12, 2),
            "mfma_frac_of_fp16_peak": round(fl / sec / 1e12 / MFMA_FP16_PEAK_TFLOPS, 4),
            "us_per_group_launch": grp,
@@ -437,8 +469,9 @@ def batched_figure(te, torch, dev, bs, K, V, args, samples=None):
     # to fp16, one MAC per weight; max rel err ~2-3e-4 against the exact default)
     sech, grph, _, _ = run_block(te, torch, dev, LAYERS, GROUPS, bs, K, V, steps, warmup,
                                  per_launch=True, mma_f16=True, samples=samples,
-                                 label=f"block batch {bs} fp16-weight mode")
+                                 label=f"block batch {bs} fp16-weight mode", graph_each=geh)
     out["mma_f16"] = {"us_per_block": round(sech * 1e6, 2),
+                      "us_per_block_one_graph_per_block": round(geh["sec"] * 1e6, 2),
                       "tflops": round(fl / sech / 1e12, 2),
                       "mfma_frac_of_fp16_peak": round(fl / sech / 1e12 / MFMA_FP16_PEAK_TFLOPS, 4),
                       "us_per_group_launch": grph,
@@ -555,11 +588,12 @@ def main():
     # in the CPU-baseline leg (check_outputs)
     samples = None if args.no_cpu_baseline else []
     log(f"[bench] block batch {B} K={K} V={V}")
+    ge = {}
     sec, us_group, us_layer, copies = run_block(te, torch, dev, LAYERS, GROUPS, B, K, V,
                                                 args.steps, args.warmup, mma_f16=args.mma_f16,
                                                 copies=args.weight_copies,
                                                 singles=not args.no_single, samples=samples,
-                                                label=f"block batch {B}")
+                                                label=f"block batch {B}", graph_each=ge)
     gbs = block_bytes / sec / 1e9
     dom_us = us_group[DOMINANT]
     dom_bytes = 2 * 12288 * 4096 * K // 8
@@ -615,6 +649,8 @@ def main():
                    "rotated_bytes": block_bytes * copies,
                    "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
                    "us_per_block": round(sec * 1e6, 2),
+                   "blocks_per_graph": copies,
+                   "us_per_block_one_graph_per_block": round(ge["sec"] * 1e6, 2),
                    "launches_per_block": [g for g, _ in GROUPS],
                    "us_per_group_launch": us_group,
                    "us_per_layer_single_launch": us_layer,
