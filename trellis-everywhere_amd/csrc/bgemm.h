@@ -80,9 +80,9 @@ __device__ __forceinline__ void bg_out_fold(const LinArgs& g, const LinMat& m, c
         const float v = (h ? hi[c] : lo[c]) * so[h];
         const long long o = static_cast<long long>(b0 + b) * m.ldy + ob * 128 + rl;
         if (g.y_f16)
-          static_cast<_Float16*>(m.y)[o] = static_cast<_Float16>(v);
+          st_wt(static_cast<_Float16*>(m.y) + o, static_cast<_Float16>(v));
         else
-          static_cast<float*>(m.y)[o] = v;
+          st_wt(static_cast<float*>(m.y) + o, v);
       }
     }
   }
@@ -366,14 +366,16 @@ __global__ __launch_bounds__((64 * BgWaves<NC, F16>::WV)) void bgemm_kernel(LinA
   }
 
   if (m.S > 1) {
-    // publish this slice's partial block; bfold_kernel adds the slices and folds
+    // publish this slice's partial block (16-byte write-through stores); bfold_kernel adds
+    // the slices and folds
     float* mypart = m.part + (static_cast<size_t>(ob * ncb + cb) * m.S + sl) * NB * 128;
     const float4_t* t4 = reinterpret_cast<const float4_t*>(tl);
+    const rsrc_t r_p = make_rsrc(mypart, static_cast<unsigned>(nbv) * 512);
     for (int i = threadIdx.x; i < nbv * 32; i += 64 * BG_WAVES) {
       const int j = (i >> 5) * (TLS / 4) + (i & 31);
       float4_t v = t4[j];
       if (NR == 2) v += t4[NR_OFF / 4 + j];
-      reinterpret_cast<float4_t*>(mypart)[i] = v;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r_p, i * 16, 0, AUX_SC1);
     }
     return;
   }
@@ -384,7 +386,7 @@ __global__ __launch_bounds__((64 * BgWaves<NC, F16>::WV)) void bgemm_kernel(LinA
 // it loads that column's 128 rows of every slice at once (S slices x 2 values per lane in
 // flight), adds them in slice order (deterministic), and folds y = sv * osc * Hb_n(t).
 // Workgroup = 4 batch columns of one (matrix, block, column block). Runs after
-// bgemm_kernel, so plain loads see its plain stores.
+// bgemm_kernel (a kernel boundary), so plain loads see its partial sums.
 template <int CB, int NC>
 __global__ __launch_bounds__(256) void bfold_kernel(LinArgs g) {
   constexpr int NB = 16 * NC, CG = NB / 4;        // workgroups per (block, column block)
@@ -438,9 +440,9 @@ __global__ __launch_bounds__(256) void bfold_kernel(LinArgs g) {
       const float v = (h ? hi : lo) * (so[h] * nrm);
       const long long o = static_cast<long long>(b0 + n) * m.ldy + row;
       if (g.y_f16)
-        static_cast<_Float16*>(m.y)[o] = static_cast<_Float16>(v);
+        st_wt(static_cast<_Float16*>(m.y) + o, static_cast<_Float16>(v));
       else
-        static_cast<float*>(m.y)[o] = v;
+        st_wt(static_cast<float*>(m.y) + o, v);
     }
   }
 }

@@ -470,9 +470,9 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
         const float v = (h ? t1 : t0) * nrm * so[h];
         const long long o = n * m.ldy + ob * 128 + rl;
         if (g.y_f16)
-          static_cast<_Float16*>(m.y)[o] = static_cast<_Float16>(v);
+          st_wt(static_cast<_Float16*>(m.y) + o, static_cast<_Float16>(v));
         else
-          static_cast<float*>(m.y)[o] = v;
+          st_wt(static_cast<float*>(m.y) + o, v);
       }
     }
     return;
@@ -561,9 +561,9 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_kernel(LinArgs g) {
         const float v = (h ? b : a) * nrm * so[h];
         const long long o = (NB > 1 ? n * m.ldy : 0) + ob * 128 + rl;
         if (g.y_f16)
-          static_cast<_Float16*>(m.y)[o] = static_cast<_Float16>(v);
+          st_wt(static_cast<_Float16*>(m.y) + o, static_cast<_Float16>(v));
         else
-          static_cast<float*>(m.y)[o] = v;
+          st_wt(static_cast<float*>(m.y) + o, v);
       }
     }
   }
