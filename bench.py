@@ -141,15 +141,32 @@ def take_samples(blk, xs, ys, layers, label, per_layer):
     return out
 
 
+def time_blocks(torch, step, copies, steps, warmup):
+    """Seconds per block of `steps` blocks, block c of a run on weight copy c: one graph holds
+    a run of `copies` blocks (a model's forward pass is captured whole, so a graph launch is
+    not charged to every block), and the timed region replays whole runs and then a graph of
+    the first `steps % copies` copies, exactly `steps` blocks between two synchronizations."""
+    run = capture(torch, lambda: [step(c) for c in range(copies)])
+    tail_n = steps % copies
+    tail = capture(torch, lambda: [step(c) for c in range(tail_n)]) if tail_n else None
+    for _ in range(max(1, math.ceil(warmup / copies))):
+        run.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps // copies):
+        run.replay()
+    if tail is not None:
+        tail.replay()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
 def run_block(te, torch, dev, layers, groups, B, K, V, steps, warmup, min_bytes=1.0e9,
               per_launch=True, mma_f16=False, copies=None, singles=True, samples=None,
               label="", sample_blocks=3, graph_each=None):
-    """Time `steps` blocks (each block's launches in order) over distinct weight copies.
-    One HIP graph holds a run of blocks, one per weight copy, as a model's forward pass is
-    captured whole: a graph launch is then not charged to every block. The timed region
-    holds exactly `steps` blocks: whole runs, then a graph of the first `steps % copies`
-    copies. Returns (seconds per step, {group: us per launch}, {layer: us per launch},
-    copies); singles=False never launches the layers one by one (a counter run then sees
+    """Time `steps` blocks (each block's launches in order) over distinct weight copies
+    (time_blocks: one graph per run of blocks, one block per copy). Returns (seconds per
+    step, {group: us per launch}, {layer: us per launch}, copies); singles=False never launches the layers one by one (a counter run then sees
     only the group launches). With a `graph_each` dict, `steps` more blocks are timed with
     one graph per block (one graph launch per block) and their seconds per block stored
     under "sec". With a `samples` list, a graph of copy 0's block is replayed after the
@@ -182,20 +199,7 @@ def run_block(te, torch, dev, layers, groups, B, K, V, steps, warmup, min_bytes=
             for name, _, _ in layers:
                 single(c, name)
     torch.cuda.synchronize()
-    run = capture(torch, lambda: [step(c) for c in range(copies)])
-    tail_n = steps % copies
-    tail = capture(torch, lambda: [step(c) for c in range(tail_n)]) if tail_n else None
-    for _ in range(max(1, math.ceil(warmup / copies))):
-        run.replay()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps // copies):
-        run.replay()
-    if tail is not None:
-        tail.replay()
-    torch.cuda.synchronize()
-    sec = (time.perf_counter() - t0) / steps
-    del run, tail
+    sec = time_blocks(torch, step, copies, steps, warmup)
     if graph_each is not None:
         graphs = [capture(torch, lambda c=c: step(c)) for c in range(copies)]
         for s in range(warmup):

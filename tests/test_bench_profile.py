@@ -1,7 +1,8 @@
 """The committed counter summary that bench.py's roofline.traffic reads: it parses, and the
 scaled bytes per gate+up launch agree with the algorithmic bytes (2 x 12288 x 4096 packed
 K=3 words), so the figure can neither vanish (a key renamed) nor drift below the bytes the
-kernel must read (a wrong calibration pass)."""
+kernel must read (a wrong calibration pass). Also bench.py's host logic that needs no GPU:
+it refuses more than one GPU, and its timed region holds exactly the requested blocks."""
 import os
 import sys
 
@@ -47,3 +48,29 @@ def test_bench_refuses_more_than_one_gpu():
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 2
     assert "one GPU" in json.loads(r.stdout.strip().splitlines()[-1])["error"]
+
+
+def test_time_blocks_times_exactly_the_steps(monkeypatch):
+    """The timed region of the block bench holds exactly `steps` blocks, block i on weight
+    copy i % copies, whatever `steps` is against the run length (whole runs, then a tail)."""
+    import types
+    log = []
+
+    class Graph:
+        def __init__(self, fn):
+            self.fn = fn
+
+        def replay(self):
+            self.fn()
+
+    monkeypatch.setattr(bench, "capture", lambda torch, fn: Graph(fn))
+    fake = types.SimpleNamespace(cuda=types.SimpleNamespace(synchronize=lambda: log.append("sync")))
+    for copies, steps, warmup in [(14, 200, 10), (14, 28, 3), (5, 3, 0), (18, 200, 20), (1, 7, 2)]:
+        log.clear()
+        sec = bench.time_blocks(fake, lambda c: log.append(c), copies, steps, warmup)
+        assert sec >= 0
+        syncs = [i for i, v in enumerate(log) if v == "sync"]
+        assert len(syncs) == 2
+        timed = log[syncs[0] + 1:syncs[1]]
+        assert timed == [i % copies for i in range(steps)], (copies, steps)
+        assert len(log[:syncs[0]]) >= max(warmup, 1)     # the warm-up replays whole runs
