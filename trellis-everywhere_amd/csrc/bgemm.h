@@ -57,9 +57,10 @@ __device__ __forceinline__ void bg_out_fold(const LinArgs& g, const LinMat& m, c
     const int b = min(wave + WAVES * c, nbv - 1);
     lo[c] = tl[b * TLS + lane];
     hi[c] = tl[b * TLS + lane + 64];
-    if (NR == 2) {
-      lo[c] += tl[NR_OFF + b * TLS + lane];
-      hi[c] += tl[NR_OFF + b * TLS + lane + 64];
+#pragma unroll
+    for (int q = 1; q < NR; ++q) {
+      lo[c] += tl[q * NR_OFF + b * TLS + lane];
+      hi[c] += tl[q * NR_OFF + b * TLS + lane + 64];
     }
     if (lane >= rows) lo[c] = 0.f;
     if (lane + 64 >= rows) hi[c] = 0.f;
@@ -108,6 +109,19 @@ template <int NC, int F16> struct BgWaves {
 template <int NC, int F16> struct BgBands {
   static constexpr int BW = (!F16 && NC == 1) ? 4 : 2;
 };
+// LDS regions of the epilogue's t[NB][TLS] partial sums, one per k-lane added in the same
+// round (the k-lanes' sums meet in KL / NR rounds). From 64 batch columns (one workgroup per
+// CU whatever its LDS) as many as the LDS holds beside the waves' packed-word buffers, up to
+// one per k-lane; below that two where they fit in the B buffers, so a kernel with few
+// registers keeps its LDS small enough for two workgroups per CU.
+constexpr int BG_LDS_WORDS = 160 * 1024 / 4;
+template <int NC> __host__ __device__ constexpr int bg_regions(int nb, int kl, int tls, int xbuf,
+                                                              int other) {
+  if (NC < 4) return 2 * nb * tls <= 2 * xbuf ? 2 : 1;
+  int r = kl;
+  while (r > 1 && r * nb * tls + other > BG_LDS_WORDS) r /= 2;
+  return r;
+}
 
 // s_setprio with a value known after unrolling (the instruction takes an immediate)
 __device__ __forceinline__ void setprio_n(int v) {
@@ -140,15 +154,17 @@ __global__ __launch_bounds__((64 * BgWaves<NC, F16>::WV)) void bgemm_kernel(LinA
   constexpr int BCH = BW * TPL * CPT;              // 16-byte chunks per wave per step
   constexpr int BLOADS = (BCH + 63) / 64;
   constexpr int BSW = BLOADS * 256;                // words per wave buffer: every lane's chunks
-  static_assert(NB * 136 <= 2 * XBUF, "epilogue t[NB][136] reuses the B buffers");
   static_assert(!F16 || (KT == 2 * KL && BW == 2), "fp16-weight mode: one tile pair per k-lane per step");
-  __shared__ __align__(16) uint32_t xsb[2 * XBUF];
-  __shared__ __align__(16) uint32_t bst[BG_WAVES * BSW];
   // epilogue: t[NB][TLS] (rows padded like the B rows, so a fragment's float4 writes
-  // spread over the banks), in two regions when they fit (k-lanes 0 + 2 and 1 + 3), else one
+  // spread over the banks) in NR regions NR_OFF floats apart over the B buffers (bg_regions:
+  // k-lanes k2 .. k2 + NR - 1 add into regions 0 .. NR - 1 in round k2 / NR)
   constexpr int TLS = 136;
-  constexpr int NR = 2 * NB * TLS <= 2 * XBUF ? 2 : 1;
+  constexpr int NR = bg_regions<NC>(NB, KL, TLS, XBUF, BG_WAVES * BSW);
   constexpr int NR_OFF = NB * TLS;
+  constexpr int XSB = 2 * XBUF > NR * NR_OFF ? 2 * XBUF : NR * NR_OFF;
+  static_assert(KL % NR == 0 && NB * TLS <= XSB, "epilogue regions");
+  __shared__ __align__(16) uint32_t xsb[XSB];
+  __shared__ __align__(16) uint32_t bst[BG_WAVES * BSW];
   float* tl = reinterpret_cast<float*>(xsb);
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -374,7 +390,8 @@ __global__ __launch_bounds__((64 * BgWaves<NC, F16>::WV)) void bgemm_kernel(LinA
     for (int i = threadIdx.x; i < nbv * 32; i += 64 * BG_WAVES) {
       const int j = (i >> 5) * (TLS / 4) + (i & 31);
       float4_t v = t4[j];
-      if (NR == 2) v += t4[NR_OFF / 4 + j];
+#pragma unroll
+      for (int q = 1; q < NR; ++q) v += t4[q * (NR_OFF / 4) + j];
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r_p, i * 16, 0, AUX_SC1);
     }
     return;
