@@ -11,7 +11,9 @@ HBM; to defeat the 256 MB Infinity Cache the steps rotate over `copies` distinct
 forward pass is captured whole, so a graph launch is not charged to every block); the
 timed region replays whole runs and then a graph of the remaining blocks, exactly `steps`
 blocks. The same blocks with one graph per block (a graph launch each) are reported
-beside it ("us_per_block_one_graph_per_block").
+beside it ("us_per_block_one_graph_per_block"). Every timed region follows at least W
+untimed blocks and at least WARM_S = 50 ms of untimed replays: the GPU's clocks ramp up over
+the first ~20-30 ms of load after idle.
 
 value = packed-weight bytes of the block / seconds per step (GB/s, algorithmic bytes
 n*k*K/8). The JSON line also carries us/layer, the dominant launch's HBM roofline (gate+up,
@@ -51,6 +53,11 @@ MLP = [("gate", 12288, 4096), ("up", 12288, 4096), ("down", 4096, 12288)]
 HBM_PEAK_GBS = 8000.0
 MFMA_FP16_PEAK_TFLOPS = 2500.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_gate_up_b1_traffic.txt")
+# Untimed replays before every timed region last at least this long: the GPU's clocks ramp
+# up over the first ~20-30 ms of load after idle (8B block at batch 1: 53.6 us in the first
+# run of 14 blocks, 51.3 in the twelfth, 47.7 at steady state; batch 64: 119.6 -> 106.7; the
+# ramp recurs after 0.5 s idle), and a timed region inside it reads the ramp, not the kernels.
+WARM_S = 0.05
 
 
 def log(msg):
@@ -141,17 +148,31 @@ def take_samples(blk, xs, ys, layers, label, per_layer):
     return out
 
 
+def warm_up(torch, replay, at_least):
+    """Untimed replays (replay(i) for i = 0, 1, ..) before a timed region: at least
+    `at_least` of them and at least WARM_S seconds of them (synchronized every few, so the
+    host clock follows the GPU's). Returns how many ran."""
+    t0 = time.perf_counter()
+    n = 0
+    while n < at_least or time.perf_counter() - t0 < WARM_S:
+        replay(n)
+        n += 1
+        if n % 4 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    return n
+
+
 def time_blocks(torch, step, copies, steps, warmup):
     """Seconds per block of `steps` blocks, block c of a run on weight copy c: one graph holds
     a run of `copies` blocks (a model's forward pass is captured whole, so a graph launch is
     not charged to every block), and the timed region replays whole runs and then a graph of
-    the first `steps % copies` copies, exactly `steps` blocks between two synchronizations."""
+    the first `steps % copies` copies, exactly `steps` blocks between two synchronizations,
+    after whole runs covering at least `warmup` blocks and WARM_S seconds (warm_up)."""
     run = capture(torch, lambda: [step(c) for c in range(copies)])
     tail_n = steps % copies
     tail = capture(torch, lambda: [step(c) for c in range(tail_n)]) if tail_n else None
-    for _ in range(max(1, math.ceil(warmup / copies))):
-        run.replay()
-    torch.cuda.synchronize()
+    warm_up(torch, lambda i: run.replay(), max(1, math.ceil(warmup / copies)))
     t0 = time.perf_counter()
     for _ in range(steps // copies):
         run.replay()
@@ -202,9 +223,7 @@ def run_block(te, torch, dev, layers, groups, B, K, V, steps, warmup, min_bytes=
     sec = time_blocks(torch, step, copies, steps, warmup)
     if graph_each is not None:
         graphs = [capture(torch, lambda c=c: step(c)) for c in range(copies)]
-        for s in range(warmup):
-            graphs[s % copies].replay()
-        torch.cuda.synchronize()
+        warm_up(torch, lambda i: graphs[i % copies].replay(), warmup)
         t0 = time.perf_counter()
         for s in range(steps):
             graphs[s % copies].replay()
@@ -227,7 +246,7 @@ def run_block(te, torch, dev, layers, groups, B, K, V, steps, warmup, min_bytes=
             # one graph holding the launch for every copy (distinct weights back to back),
             # HIP events on the launch stream around its replays
             g = capture(torch, lambda: [fn_for_copy(c) for c in range(copies)])
-            g.replay()
+            warm_up(torch, lambda i: g.replay(), 1)
             e0 = torch.cuda.Event(enable_timing=True)
             e1 = torch.cuda.Event(enable_timing=True)
             e0.record()
@@ -397,7 +416,7 @@ def extras(te, torch, dev, steps, K=4, samples=None):
             fn(c)
         torch.cuda.synchronize()
         gr = capture(torch, lambda: [fn(c) for c in range(copies)])
-        gr.replay()
+        warm_up(torch, lambda i: gr.replay(), 1)
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         reps = max(2, steps // copies)
@@ -654,6 +673,7 @@ def main():
                    "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
                    "us_per_block": round(sec * 1e6, 2),
                    "blocks_per_graph": copies,
+                   "warmup_s_min": WARM_S,
                    "us_per_block_one_graph_per_block": round(ge["sec"] * 1e6, 2),
                    "launches_per_block": [g for g, _ in GROUPS],
                    "us_per_group_launch": us_group,

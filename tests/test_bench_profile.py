@@ -70,7 +70,22 @@ def test_time_blocks_times_exactly_the_steps(monkeypatch):
         sec = bench.time_blocks(fake, lambda c: log.append(c), copies, steps, warmup)
         assert sec >= 0
         syncs = [i for i, v in enumerate(log) if v == "sync"]
-        assert len(syncs) == 2
-        timed = log[syncs[0] + 1:syncs[1]]
+        timed = log[syncs[-2] + 1:syncs[-1]]               # between the last two syncs
         assert timed == [i % copies for i in range(steps)], (copies, steps)
-        assert len(log[:syncs[0]]) >= max(warmup, 1)     # the warm-up replays whole runs
+        warm = [v for v in log[:syncs[-2]] if v != "sync"]
+        assert len(warm) >= max(warmup, 1) and len(warm) % copies == 0   # whole runs
+
+
+def test_warm_up_lasts_the_count_and_the_time(monkeypatch):
+    import time
+    import types
+    monkeypatch.setattr(bench, "WARM_S", 0.02)
+    calls = []
+    fake = types.SimpleNamespace(cuda=types.SimpleNamespace(synchronize=lambda: None))
+    t0 = time.perf_counter()
+    n = bench.warm_up(fake, lambda i: calls.append(i), 3)
+    assert time.perf_counter() - t0 >= 0.02 and n == len(calls) >= 3
+    assert calls == list(range(n))
+    calls.clear()
+    monkeypatch.setattr(bench, "WARM_S", 0.0)
+    assert bench.warm_up(fake, lambda i: calls.append(i), 5) == 5 and calls == list(range(5))
