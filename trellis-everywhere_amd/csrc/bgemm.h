@@ -404,12 +404,13 @@ __global__ __launch_bounds__((64 * BgWaves<NC, F16>::WV)) void bgemm_kernel(LinA
 // flight), adds them in slice order (deterministic), and folds y = sv * osc * Hb_n(t).
 // Workgroup = 4 batch columns of one (matrix, block, column block). Runs after
 // bgemm_kernel (a kernel boundary), so plain loads see its partial sums.
-template <int CB, int NC>
+template <int CB, int NC, bool SINGLE>
 __global__ __launch_bounds__(256) void bfold_kernel(LinArgs g) {
   constexpr int NB = 16 * NC, CG = NB / 4;        // workgroups per (block, column block)
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int fi = blockIdx.x / CG, cg = blockIdx.x % CG;
-  const int mi = locate_fold(g, fi);
+  // a one-matrix launch reads its matrix's fields in the first round of argument loads
+  const int mi = SINGLE ? 0 : locate_fold(g, fi);
   const LinMat& m = g.m[mi];
   const int ncb = (g.batch + NB - 1) / NB;
   const int local = fi - m.fold0;

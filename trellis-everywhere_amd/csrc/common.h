@@ -352,12 +352,13 @@ __device__ __forceinline__ int xf_pair_slot(int e) {
 // block 517 -> 503.5 us, 360 -> 347.5 in the fp16-weight mode; at 128 rows no change.
 __host__ __device__ constexpr int xfold_rows(int batch) { return batch >= 256 ? 4 : 1; }
 #ifdef TRELLIS_XFOLD_DEFINE
-template <int XFOLD_ROWS>
+template <int XFOLD_ROWS, bool SINGLE>
 __global__ __launch_bounds__(256) void xfold_kernel(LinArgs g) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int job = blockIdx.x * 4 + wave;
   if (job >= g.total) return;
-  const int mi = locate_mat(g, job, true);
+  // a one-matrix launch reads its matrix's fields in the first round of argument loads
+  const int mi = SINGLE ? 0 : locate_mat(g, job, true);
   const LinMat& m = g.m[mi];
   const int local = job - m.chunk0;
   const int nch = (m.k + 127) / 128;

@@ -32,11 +32,24 @@ int launch_bfold(int cb, int nc, int nfold, const LinArgs& g, hipStream_t st);
 template <int CB>
 static int launch_bfold_cb(int nc, int nfold, const LinArgs& g, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(nfold * 4 * nc));
+  const bool one = g.nmat == 1;
   switch (nc) {
-    case 1: hipLaunchKernelGGL((bfold_kernel<CB, 1>), grid, dim3(256), 0, st, g); break;
-    case 2: hipLaunchKernelGGL((bfold_kernel<CB, 2>), grid, dim3(256), 0, st, g); break;
-    case 4: hipLaunchKernelGGL((bfold_kernel<CB, 4>), grid, dim3(256), 0, st, g); break;
-    default: hipLaunchKernelGGL((bfold_kernel<CB, 8>), grid, dim3(256), 0, st, g); break;
+    case 1:
+      if (one) hipLaunchKernelGGL((bfold_kernel<CB, 1, true>), grid, dim3(256), 0, st, g);
+      else hipLaunchKernelGGL((bfold_kernel<CB, 1, false>), grid, dim3(256), 0, st, g);
+      break;
+    case 2:
+      if (one) hipLaunchKernelGGL((bfold_kernel<CB, 2, true>), grid, dim3(256), 0, st, g);
+      else hipLaunchKernelGGL((bfold_kernel<CB, 2, false>), grid, dim3(256), 0, st, g);
+      break;
+    case 4:
+      if (one) hipLaunchKernelGGL((bfold_kernel<CB, 4, true>), grid, dim3(256), 0, st, g);
+      else hipLaunchKernelGGL((bfold_kernel<CB, 4, false>), grid, dim3(256), 0, st, g);
+      break;
+    default:
+      if (one) hipLaunchKernelGGL((bfold_kernel<CB, 8, true>), grid, dim3(256), 0, st, g);
+      else hipLaunchKernelGGL((bfold_kernel<CB, 8, false>), grid, dim3(256), 0, st, g);
+      break;
   }
   return hipGetLastError() == hipSuccess ? 0 : 13;
 }

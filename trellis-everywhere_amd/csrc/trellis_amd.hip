@@ -322,10 +322,15 @@ int launch_gemv(int K, int cb, int V, int kc, const LinArgs& g, hipStream_t st) 
 int launch_xfold(LinArgs& g, int folds, hipStream_t st) {
   const int items = g.total;
   g.total = folds;
-  if (xfold_rows(g.batch) == 4)
-    hipLaunchKernelGGL(xfold_kernel<4>, dim3(static_cast<unsigned>((folds + 3) / 4)), dim3(256), 0, st, g);
-  else
-    hipLaunchKernelGGL(xfold_kernel<1>, dim3(static_cast<unsigned>((folds + 3) / 4)), dim3(256), 0, st, g);
+  const dim3 grid(static_cast<unsigned>((folds + 3) / 4));
+  const bool one = g.nmat == 1;
+  if (xfold_rows(g.batch) == 4) {
+    if (one) hipLaunchKernelGGL((xfold_kernel<4, true>), grid, dim3(256), 0, st, g);
+    else hipLaunchKernelGGL((xfold_kernel<4, false>), grid, dim3(256), 0, st, g);
+  } else {
+    if (one) hipLaunchKernelGGL((xfold_kernel<1, true>), grid, dim3(256), 0, st, g);
+    else hipLaunchKernelGGL((xfold_kernel<1, false>), grid, dim3(256), 0, st, g);
+  }
   g.total = items;
   return hipGetLastError() == hipSuccess ? TRELLIS_OK : TRELLIS_ERR_LAUNCH;
 }
