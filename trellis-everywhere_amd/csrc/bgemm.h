@@ -131,7 +131,7 @@ __device__ __forceinline__ void setprio_n(int v) {
   else __builtin_amdgcn_s_setprio(0);
 }
 
-template <int K, int CB, int V, int NC, int F16>
+template <int K, int CB, int V, int NC, int F16, bool SINGLE>
 __global__ __launch_bounds__((64 * BgWaves<NC, F16>::WV)) void bgemm_kernel(LinArgs g) {
   constexpr int BG_WAVES = BgWaves<NC, F16>::WV;
   constexpr int NWK = 8 * K;
@@ -169,7 +169,8 @@ __global__ __launch_bounds__((64 * BgWaves<NC, F16>::WV)) void bgemm_kernel(LinA
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int bg = wave % NG, kl = wave / NG;
-  const int mi = locate_mat(g, blockIdx.x, false);
+  // a one-matrix launch (SINGLE) reads its matrix's fields in the first argument round
+  const int mi = SINGLE ? 0 : locate_mat(g, blockIdx.x, false);
   const LinMat& m = g.m[mi];
   {
     // the matrix's fields that the set-up needs, loaded in one round (the argument segment

@@ -69,10 +69,14 @@ static int launch_gemv_nb(int kc, const LinArgs& g, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(g.total));
   // 16 rows: stages of 8 tiles (two 16-tile ring slots do not fit beside their activations)
   constexpr int KC_WIDE = NB == 16 ? 8 : 16;
-  if (kc == 8)
-    hipLaunchKernelGGL((gemv_kernel<K, CB, V, 8, NB>), grid, dim3(64 * GEMV_WAVES), 0, st, g);
-  else
-    hipLaunchKernelGGL((gemv_kernel<K, CB, V, KC_WIDE, NB>), grid, dim3(64 * GEMV_WAVES), 0, st, g);
+  const bool one = g.nmat == 1;
+  if (kc == 8) {
+    if (one) hipLaunchKernelGGL((gemv_kernel<K, CB, V, 8, NB, true>), grid, dim3(64 * GEMV_WAVES), 0, st, g);
+    else hipLaunchKernelGGL((gemv_kernel<K, CB, V, 8, NB, false>), grid, dim3(64 * GEMV_WAVES), 0, st, g);
+  } else {
+    if (one) hipLaunchKernelGGL((gemv_kernel<K, CB, V, KC_WIDE, NB, true>), grid, dim3(64 * GEMV_WAVES), 0, st, g);
+    else hipLaunchKernelGGL((gemv_kernel<K, CB, V, KC_WIDE, NB, false>), grid, dim3(64 * GEMV_WAVES), 0, st, g);
+  }
   return hipGetLastError() == hipSuccess ? 0 : 13;
 }
 
@@ -104,12 +108,17 @@ int launch_gemv_k(int cb, int V, int kc, const LinArgs& g, hipStream_t st) {
 template <int K, int CB, int V, int F16>
 static int launch_bgemm_nc(int nc, const LinArgs& g, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(g.total));
+  const bool one = g.nmat == 1;
+#define TRELLIS_BG_LAUNCH(NCV) \
+  if (one) hipLaunchKernelGGL((bgemm_kernel<K, CB, V, NCV, F16, true>), grid, dim3(64 * BgWaves<NCV, F16>::WV), 0, st, g); \
+  else hipLaunchKernelGGL((bgemm_kernel<K, CB, V, NCV, F16, false>), grid, dim3(64 * BgWaves<NCV, F16>::WV), 0, st, g);
   switch (nc) {
-    case 1: hipLaunchKernelGGL((bgemm_kernel<K, CB, V, 1, F16>), grid, dim3(64 * BgWaves<1, F16>::WV), 0, st, g); break;
-    case 2: hipLaunchKernelGGL((bgemm_kernel<K, CB, V, 2, F16>), grid, dim3(64 * BgWaves<2, F16>::WV), 0, st, g); break;
-    case 4: hipLaunchKernelGGL((bgemm_kernel<K, CB, V, 4, F16>), grid, dim3(64 * BgWaves<4, F16>::WV), 0, st, g); break;
-    default: hipLaunchKernelGGL((bgemm_kernel<K, CB, V, 8, F16>), grid, dim3(64 * BgWaves<8, F16>::WV), 0, st, g); break;
+    case 1: TRELLIS_BG_LAUNCH(1) break;
+    case 2: TRELLIS_BG_LAUNCH(2) break;
+    case 4: TRELLIS_BG_LAUNCH(4) break;
+    default: TRELLIS_BG_LAUNCH(8) break;
   }
+#undef TRELLIS_BG_LAUNCH
   return hipGetLastError() == hipSuccess ? 0 : 13;
 }
 
