@@ -90,16 +90,18 @@ __device__ __forceinline__ void bg_out_fold(const LinArgs& g, const LinMat& m, c
 }
 
 // k-step: 16 tile columns for 16 batch columns (half the barriers; the 8B gate+up group at
-// batch 16: 29.1 -> 27.9 us), 8 for up to 64, 4 for 128 (LDS holds two B steps); always 8
-// in the fp16-weight mode, whose B words are half as many per column
+// batch 16: 29.1 -> 27.9 us), 8 for up to 64, 6 for 128 (two per k-lane over three
+// k-lanes; LDS holds two B steps; a k-range's last step may be partial); always 8 in the
+// fp16-weight mode, whose B words are half as many per column
 template <int NC, int F16> struct BgStep {
-  static constexpr int KT = F16 ? 8 : NC == 1 ? 16 : NC <= 4 ? 8 : 4;
+  static constexpr int KT = F16 ? 8 : NC == 1 ? 16 : NC <= 4 ? 8 : 6;
 };
-// waves per workgroup: 16 (four per SIMD), or 8 (two per SIMD, 256 registers each) for the
-// exact mode's 128-column blocks, whose 8 fragments and 16 accumulators per wave do not fit
-// a quarter of a SIMD's registers
+// waves per workgroup: 16 (four per SIMD), or 12 (three per SIMD, up to 168 registers each)
+// for the exact mode's 128-column blocks, whose 8 fragments and 16 accumulators per wave
+// (~150 registers) do not fit a quarter of a SIMD's registers (against 8 waves, two per
+// SIMD: the 8B block at a 512 prefill 463.4 -> 452.2 us, gate+up at 128 rows 69.4 -> 64.9)
 template <int NC, int F16> struct BgWaves {
-  static constexpr int WV = (!F16 && NC == 8) ? 8 : 16;
+  static constexpr int WV = (!F16 && NC == 8) ? 12 : 16;
 };
 // bands per wave: 4 at 16 batch columns (8 k-lanes: each B fragment read from LDS feeds 4
 // bands instead of 2; the 8B gate+up group at batch 16 27.8 -> 26.6-27.1 us), otherwise 2

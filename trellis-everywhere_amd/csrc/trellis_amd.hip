@@ -169,7 +169,7 @@ int gemv_kr(const trellis_desc* const* W, int count, int batch) {
 // mode, else 4), run by one workgroup per CU (16 waves; 8 for the exact mode's 128-column
 // blocks). kr minimises ceil(items/CUs) x the per-SIMD work of an item (2 bands x kr tiles
 // x (decode ~61 + NC MFMAs x ~19 cycles; fp16-weight mode ~75 + NC x ~10; ~240 for the
-// exact mode's 128-column blocks, whose two waves per SIMD hide less: with 258 the 8B down
+// exact mode's 128-column blocks, whose three waves per SIMD hide less: with 258 the 8B down
 // launch at 256 and 512 rows took 64 columns, 71.9 and 134 us, against 66.2 and 124 at 128
 // columns)) plus, with split-K,
 // the bfold_kernel launch (~1.5 us) and the partial blocks it moves (S x rows x NB x 4
@@ -179,7 +179,7 @@ static int bgemm_kr_cost(const trellis_desc* const* W, int count, int batch, int
                          long long* cost) {
   int maxt = 0;
   for (int i = 0; i < count; ++i) maxt = W[i]->k_in / 16 > maxt ? W[i]->k_in / 16 : maxt;
-  const int kt = f16 ? 8 : nc == 1 ? 16 : nc <= 4 ? 8 : 4;   // BgStep<nc, f16>::KT
+  const int kt = f16 ? 8 : nc == 1 ? 16 : nc <= 4 ? 8 : 6;   // BgStep<nc, f16>::KT
   // per band-tile SIMD cycles: the decode and NC MFMAs (the fp16-weight mode decodes a
   // little more and issues half the MFMAs)
   const long long tile_cost = f16 ? 75 + 10 * nc : nc == 8 ? 240 : 61 + 19 * nc;
@@ -220,7 +220,7 @@ int bgemm_kr(const trellis_desc* const* W, int count, int batch, int nc, bool f1
 }
 
 // Column-block width: 16, 32 or 64 columns up to batch 64; above, the fp16-weight mode
-// takes 128, and the exact mode 64 (four waves per SIMD) or 128 (two waves per SIMD, each
+// takes 128, and the exact mode 64 (four waves per SIMD) or 128 (three waves per SIMD, each
 // tile decoded half as often), whichever the cost model above finds cheaper for the group
 // (8B block at batch 512: q/k/v and gate+up at 128 columns, 100 -> 87 and 277 -> 243 us;
 // o stays at 64, where 128 measured 53 -> 57 us; one gate projection at batch 96 stays at 64,
