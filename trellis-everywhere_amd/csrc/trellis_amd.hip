@@ -166,12 +166,12 @@ int gemv_kr(const trellis_desc* const* W, int count, int batch) {
 // Batch >= 2 (bgemm_kernel): NC 16-column batch chunks per workgroup (up to 128 columns),
 // a work item is one 128-row block x one column block x one k-range of kr tile columns
 // (a multiple of the k-step: 16 tiles at 16 columns, 8 up to 64 and in the fp16-weight
-// mode, else 4), run by one workgroup per CU (16 waves; 8 for the exact mode's 128-column
+// mode, else 6), run by one workgroup per CU (16 waves; 12 for the exact mode's 128-column
 // blocks). kr minimises ceil(items/CUs) x the per-SIMD work of an item (2 bands x kr tiles
-// x (decode ~61 + NC MFMAs x ~19 cycles; fp16-weight mode ~75 + NC x ~10; ~240 for the
-// exact mode's 128-column blocks, whose three waves per SIMD hide less: with 258 the 8B down
-// launch at 256 and 512 rows took 64 columns, 71.9 and 134 us, against 66.2 and 124 at 128
-// columns)) plus, with split-K,
+// x (decode ~61 + NC MFMAs x ~19 cycles; fp16-weight mode ~75 + NC x ~10; ~225 for the
+// exact mode's 128-column blocks at three waves per SIMD, fitted to a sweep of both widths
+// on the 8B block's launches at 128-512 rows, where it picks the faster width for all but
+// q/k/v at 128 and 192 rows, ~3 us each)) plus, with split-K,
 // the bfold_kernel launch (~1.5 us) and the partial blocks it moves (S x rows x NB x 4
 // bytes written and read at ~2.5 KB per cycle), plus a start-up latency per round after
 // the first. TRELLIS_BGEMM_KR forces a value, TRELLIS_BGEMM_NC the column-block width.
@@ -182,7 +182,7 @@ static int bgemm_kr_cost(const trellis_desc* const* W, int count, int batch, int
   const int kt = f16 ? 8 : nc == 1 ? 16 : nc <= 4 ? 8 : 6;   // BgStep<nc, f16>::KT
   // per band-tile SIMD cycles: the decode and NC MFMAs (the fp16-weight mode decodes a
   // little more and issues half the MFMAs)
-  const long long tile_cost = f16 ? 75 + 10 * nc : nc == 8 ? 240 : 61 + 19 * nc;
+  const long long tile_cost = f16 ? 75 + 10 * nc : nc == 8 ? 225 : 61 + 19 * nc;
   const int cap = ((maxt + kt - 1) / kt) * kt;
   const long long cus = device_cus();
   const long long ncb = (batch + 16 * nc - 1) / (16 * nc);
