@@ -1,13 +1,14 @@
 // bgemm.h — batched packed linear for gfx950 (batch 2 .. prefill): decode once, reuse
 // across the batch.
 //
-// A workgroup of 16 waves (8 for the exact mode's 128-column blocks) owns one 128-row
+// A workgroup of 16 waves (12 for the exact mode's 128-column blocks) owns one 128-row
 // output block (the out-dim Hadamard block) x NB = 16*NC batch columns x one k-range of
-// `kr` tile columns, walked in steps of KT tiles (16 at 16 columns, 8, or 4 at 128
-// columns). Wave w = (band group bg = w % NG, k-lane kl = w / NG), a band group being
-// BW = 2 or 4 adjacent bands (NG = 8 / BW groups, KL = waves / NG k-lanes): the waves of a
-// SIMD share a band group and split every step's tiles between them (tile j of a step
-// belongs to k-lane j % KL), so a SIMD has four (or two) waves to switch between:
+// `kr` tile columns, walked in steps of KT tiles (16 at 16 columns, 8 up to 64 and in the
+// fp16-weight mode, 6 for the exact mode's 128 columns). Wave w = (band group
+// bg = w % NG, k-lane kl = w / NG), a band group being BW = 2 or 4 adjacent bands
+// (NG = 8 / BW groups, KL = waves / NG k-lanes): the waves of a SIMD share a band group and
+// split every step's tiles between them (tile j of a step belongs to k-lane j % KL), so a
+// SIMD has four (or three) waves to switch between:
 //   * the B tile of a step (xf[batch cols][KT*16] as (x, x) fp16 pairs written by
 //     xfold_kernel) is loaded two steps ahead into registers by all the threads, stored
 //     to one half of a double-buffered LDS area, and read by every wave: each fragment
