@@ -6,10 +6,13 @@
 // (rb, jb: first row / column of r's and j's Hadamard blocks; H entries (-1)^popcount(a&b)).
 // The two Hadamard sums commute, so every weight of the B_n x B_k block is decoded once
 // per (token, column block): one workgroup per (token, column block), 4 waves.
-//   * wave w takes the bands b = w, w + 4, ... of the row block; lane (row rl = l%16,
-//     column group g = l/16) decodes 4 weights of each tile (the same window/codebook
-//     code as the matmul kernels) and accumulates sign(rr, 16b + rl) * w per column, so a
-//     lane holds 4 columns of each of the block's tile columns. MCG/3INST: one
+//   * wave w takes the bands b = w, w + 4 of the row block; it loads their tiles' packed
+//     words as 16-byte chunks into a wave-private LDS buffer (one chunk per lane and load;
+//     each lane loading its window words straight from global memory, two 4-byte gathers
+//     per tile, measured slower in the batched kernel), then lane (row rl = l%16, column
+//     group g = l/16) decodes 4 weights of each tile (the same window/codebook code as the
+//     matmul kernels) and accumulates sign(rr, 16b + rl) * w per column, so a lane holds 4
+//     columns of each of the block's tile columns. MCG/3INST: one
 //     v_dot2_f32_f16 of the raw (hi, lo) fp16 pair with (sign, sign) per weight (the
 //     products are exact; hi + lo is the reference's exact fp32 sum); 1MAD: the integer
 //     (y - 510) * sign, exact in fp32, divided by 147.800537109375 once per output;
@@ -40,7 +43,9 @@ struct EmbedArgs {
 template <int K, int CB, int V>
 __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
   constexpr int NWK = 8 * K;
+  constexpr int WBUF = 2 * 8 * NWK;                 // words of two bands x 8 tiles
   __shared__ float colsum[4][128];
+  __shared__ __align__(16) uint32_t wbuf[4][WBUF];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int t = blockIdx.x / a.nblk, jblk = blockIdx.x % a.nblk;
   const int jb = jblk * a.block_in;                 // first column of the block
@@ -52,6 +57,27 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
   const int rl = lane & 15, g = lane >> 4;
   const QuadPos qp = quad_pos_v<K, V>(rl, g);
 
+  // this wave's bands' tiles of the column block to LDS: band slot s (band wave + 4s)
+  // holds words [s * ntc * NWK, (s + 1) * ntc * NWK); a band past the block reads zeros
+  uint32_t* mybuf = wbuf[wave];
+  {
+    const int cpb = ntc * NWK / 4;                  // 16-byte chunks per band
+    const rsrc_t r_bits = make_rsrc(a.bits + static_cast<size_t>(rb / 16) * a.tiles_in * NWK,
+                                    static_cast<unsigned>(nbands * a.tiles_in * NWK * 4));
+#pragma unroll
+    for (int q = 0; q < (WBUF / 4 + 63) / 64; ++q) {
+      const int ch = lane + 64 * q;
+      const int sb = ch / cpb, c = ch % cpb;
+      const int band = wave + 4 * sb;
+      const unsigned off = ch < 2 * cpb && band < nbands
+                               ? static_cast<unsigned>(((band * a.tiles_in + jb / 16) * NWK + 4 * c) * 4)
+                               : RSRC_OOB;
+      const u32x4_t v = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                        r_bits, static_cast<int>(off), 0, AUX_NT));
+      if (ch < 2 * cpb) *reinterpret_cast<u32x4_t*>(mybuf + 4 * ch) = v;
+    }
+  }
+
   float acc[8][4];
 #pragma unroll
   for (int tc = 0; tc < 8; ++tc)
@@ -61,7 +87,7 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
     const int c = 16 * b + rl;                       // row within the row block
     const float sgn = (__builtin_popcount(rr & c) & 1) ? -1.f : 1.f;
     const half2_t s2 = {static_cast<_Float16>(sgn), static_cast<_Float16>(sgn)};
-    const uint32_t* band = a.bits + (static_cast<size_t>(rb / 16 + b) * a.tiles_in + jb / 16) * NWK;
+    const uint32_t* band = mybuf + ((b - wave) / 4) * ntc * NWK;
 #pragma unroll
     for (int tc = 0; tc < 8; ++tc) {
       if (tc < ntc) {
